@@ -1,0 +1,168 @@
+/*
+ * dsa_indexer.h -- C ABI of the MI355X (gfx950) DeepSeek-Sparse-Attention indexer path:
+ * paged fp8 K-cache gather/dequant, MQA indexer logits on fp8 MFMA, and the exact top-2048
+ * select with its page-table transform.
+ *
+ * Conventions shared by every entry point:
+ *   - all pointers are device pointers unless stated; sizes and strides are in elements of the
+ *     pointed-to type unless the name ends in `_bytes`;
+ *   - work is enqueued on `stream` and never synchronised; launch shapes depend only on the
+ *     scalar arguments, so every call can be captured into a hipGraph;
+ *   - no entry point allocates device memory: workspaces are passed in by the caller, sized by
+ *     the matching *_workspace_bytes query, and cleared on device by the entry point itself;
+ *   - return value: DSA_OK, or an error code with a message available from dsa_last_error()
+ *     (thread-local, valid until the next call on the same thread).
+ *
+ * K-cache layout (the indexer's 132-byte/token paged layout): page p starts at
+ * kv_cache + p * page_stride_bytes and holds 64 tokens as [64 x 128 fp8 e4m3fn][64 x fp32 scale].
+ * A token slot id is page * 64 + offset.
+ */
+#ifndef DSA_INDEXER_H_
+#define DSA_INDEXER_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  DSA_OK = 0,
+  DSA_ERR_INVALID = 1,   /* an argument violates the documented contract */
+  DSA_ERR_WORKSPACE = 2, /* the workspace passed in is smaller than required */
+  DSA_ERR_LAUNCH = 3,    /* the HIP runtime rejected a launch */
+};
+
+#define DSA_PAGE_TOKENS 64
+#define DSA_HEAD_DIM 128
+#define DSA_TOPK 2048
+
+/* Message describing the last error returned on this thread ("" after success). */
+const char* dsa_last_error(void);
+
+/* Number of compute units of the current device (used by the split policy of the top-k). */
+int dsa_device_cu_count(int* n_cu);
+
+/* ---------------------------------------------------------------------------------------------
+ * Paged K-cache dequant, indexer layout (132 B/token).
+ *   out[i, 0:128] = bf16_rne(f32(fp8[slot_i, :]) * scale[slot_i])
+ * Replaces the role of sglang's dequantize_k_cache_paged for the indexer cache; its numerics
+ * follow prefill/patches/dequant_k_cache.py.diff:30-36 (fp32 product of the fp8 value and its
+ * scale, rounded once to bf16).  slots: int32 [n_tokens]; out: bf16 [n_tokens, >=128] with row
+ * stride out_stride (elements).  page_stride_bytes % 16 == 0 and >= 64 * 132.
+ */
+int dsa_dequant_k_paged(const uint8_t* kv_cache, int64_t page_stride_bytes, const int32_t* slots,
+                        int64_t n_tokens, uint16_t* out, int64_t out_stride, hipStream_t stream);
+
+/* Same as dsa_dequant_k_paged, but gathers into contiguous fp8 + fp32 scale buffers without
+ * dequantising (the layout the prefill logits path can consume): k8 [n_tokens, 128] u8,
+ * scale [n_tokens] f32. */
+int dsa_gather_k_paged(const uint8_t* kv_cache, int64_t page_stride_bytes, const int32_t* slots,
+                       int64_t n_tokens, uint8_t* k8, float* scale, hipStream_t stream);
+
+/* MLA 656-byte slot dequant (prefill/patches/dequant_k_cache.py.diff:16-42,51-69):
+ * slot = [512 fp8][4 x fp32 group scales][64 bf16 rope];
+ *   out[i, 0:512]   = bf16_rne(f32(fp8[src, j]) * scale[src, j / 128])
+ *   out[i, 512:576] = rope[src]
+ * cache: u8 [pool, >=656] with row stride cache_stride_bytes (% 16 == 0); slots int32 [n];
+ * out bf16 [n, >=576] with row stride out_stride (elements, % 8 == 0). */
+int dsa_dequant_mla_paged(const uint8_t* cache, int64_t cache_stride_bytes, const int32_t* slots,
+                          int64_t n_tokens, uint16_t* out, int64_t out_stride, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Indexer q quantisation (the step sglang runs before the paged logits; the per-token fp8
+ * convention is hcu_ops/csrc/norm_quant.cu:13-14 applied per (row, head)):
+ *   sq = absmax(q[r,h,:]) / 448;  q8[r,h,:] = fp8_rne(q * (448 / absmax));  w_eff[r,h] = w[r,h] * sq
+ * (absmax == 0 gives q8 = 0 and w_eff = 0).  q_bf16 [rows, heads, 128] contiguous; w [rows, heads]
+ * f32; q8 [rows, heads, 128] u8; w_eff [rows, heads] f32. */
+int dsa_quant_q_fp8(const uint16_t* q_bf16, const float* w, int64_t rows, int heads, uint8_t* q8,
+                    float* w_eff, hipStream_t stream);
+
+/* Indexer K-cache writer: quantises k (bf16 [n_tokens, 128]) per token with absmax/448 and
+ * stores fp8 + fp32 scale at slots[i] in the 132-B paged layout. */
+int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* slots,
+                      uint8_t* kv_cache, int64_t page_stride_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Paged MQA indexer logits for decode (replaces hcu_ops _C.mqa_logits_hist,
+ * hcu_ops/csrc/mqa_hist.cu:324-405, and lightop page_mqa_logits_sparse_mask[_grouped]):
+ *   logits[r, t] = scale[t] * sum_h w[r, h] * relu(sum_d q8[r, h, d] * k8[t, d])   (t < len[r])
+ *   mask[r, t/16] bit t%16 = t < len[r] && bits(logits[r, t]) != 0
+ * len[r] = clamp(context_lens[r], 0, width).  Rows come in groups of `group_size` consecutive
+ * rows that share the block table row of the group's first row (mqa_hist.cu:93-95,162).
+ * q8 [B, heads, 128] u8 (fp8 e4m3fn), w [B, heads] f32, context_lens [B] i32,
+ * block_table [B, bt_pages] i32 with row stride bt_stride, width == bt_pages * 64 (mqa_hist.cu:346),
+ * logits [B, width] f32 with row stride logits_stride; entries t >= len[r] are not written.
+ * mask [B, width / 16] i16 with row stride mask_stride: every word is written.
+ * heads in {32, 64}; B % group_size == 0; rows_per_cta divides group_size and is in {1,2,3,4}.
+ * pages_per_cta <= 0 picks the default.
+ * hist_lens (nullable, int32 [B]) with hist_ws (int32 [B * (2 * 4096 + 2)]): also build pass 1
+ * of the top-k (12-bit key histogram + positive / zero counts of every row whose
+ * min(hist_lens[r], width) > 2048) into hist_ws, in the layout dsa_topk_transform_pre consumes. */
+int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t batch,
+                          int group_size, const uint8_t* kv_cache, int64_t page_stride_bytes,
+                          const int32_t* context_lens, const int32_t* block_table,
+                          int64_t bt_stride, int64_t bt_pages, float* logits,
+                          int64_t logits_stride, int16_t* mask, int64_t mask_stride,
+                          int rows_per_cta, int pages_per_cta, const int32_t* hist_lens,
+                          int32_t* hist_ws, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Prefill MQA indexer logits (the role of the prefill indexer's fp8 logits kernel, sglang
+ * `_mqa_logits`, not vendored): rows attend to keys of one paged request:
+ *   logits[r, t] = scale[t] * sum_h w[r, h] * relu(q8[r, h, :] . k8[t, :])   for t < len[r]
+ * where key t lives at slot block_table[t / 64] * 64 + t % 64 of kv_cache.  len [rows] i32
+ * (causal: prefix + i + 1), clamped to width.  Entries t >= len[r] are not written.
+ * q8 [rows, heads, 128] u8; w [rows, heads] f32; block_table [>= ceil(width / 64)] i32;
+ * logits [rows, width] f32 with row stride logits_stride. */
+int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int heads, int64_t rows,
+                           const uint8_t* kv_cache, int64_t page_stride_bytes,
+                           const int32_t* block_table, int64_t bt_pages, const int32_t* lens,
+                           float* logits, int64_t logits_stride, int64_t width,
+                           hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Exact top-2048 + page-table transform over (sparse-mask) indexer logits (replaces hcu_ops
+ * _C.sparse_mask_topk_transform[_split][_pre], hcu_ops/csrc/sparse_mask_topk.cu:896-1051, and
+ * lightop fast_topk_transform_sparse_mask_fused).
+ * For row r with len = min(lengths[r], width):
+ *   len <= 2048: out[r, i] = i < len ? page_table[pr, i] : -1
+ *   otherwise:   out[r, :] holds page_table[pr, t] for the 2048 tokens t < len with the largest
+ *                keys, ties at the threshold going to the lower t (sparse_mask_topk.cu:1-7).
+ * A token whose mask bit is clear counts as +0 and its score is never used (the storage may be
+ * garbage); mask == NULL means every score below len is valid.  The key of a score x is
+ * (bits(x) & 0x80000000) ? ~bits(x) : bits(x) | 0x80000000 (sparse_mask_topk.cu:40-43).
+ * The page-table row pr of score row r is r when cu_seqlens_q == NULL (decode layout), else the
+ * request b with cu_seqlens_q[b] <= r < cu_seqlens_q[b+1] (n_req + 1 entries; varlen prefill).
+ * Only the selected set is the contract; the order within a row is unspecified.
+ * score f32 [rows, width] row stride score_stride; mask i16 [rows, ceil(width/16)] row stride
+ * mask_stride; lengths i32 [rows]; page_table i32 with pt_cols entries per row (tokens at or past
+ * pt_cols map to -1) and row stride pt_stride; out i32 [rows, 2048].
+ * max_splits: CTAs a row may be split over (1 = one CTA per row).
+ */
+size_t dsa_topk_workspace_bytes(int64_t rows, int64_t width, int max_splits, int n_cu);
+int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
+                       const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
+                       int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
+                       const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                       void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream);
+
+/* dsa_topk_transform with pass 1 (histogram and counts) already built into hist_ws by
+ * dsa_mqa_logits_decode(hist_lens = lengths) (replaces
+ * _C.sparse_mask_topk_transform_split_pre, sparse_mask_topk.cu:986-1051).  hist_ws is the
+ * int32 [rows * (2 * 4096 + 2)] buffer given to the logits call; `workspace` as above. */
+int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t width,
+                           const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
+                           int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
+                           const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                           const int32_t* hist_ws, void* workspace, size_t workspace_bytes,
+                           int32_t* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_INDEXER_H_ */

@@ -1,0 +1,117 @@
+// Shared constants, device helpers and host-side status plumbing of the gfx950 DSA indexer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/dsa_indexer.h"
+
+namespace dsa {
+
+constexpr int kWave = 64;
+constexpr int kPage = DSA_PAGE_TOKENS;          // tokens per K-cache page
+constexpr int kHeadDim = DSA_HEAD_DIM;          // fp8 bytes per K token / q head
+constexpr int kTokBytes = kHeadDim + 4;         // fp8 row + fp32 scale
+constexpr int kPageFp8Bytes = kPage * kHeadDim; // scales start here inside a page
+constexpr int kPageBytes = kPage * kTokBytes;   // 8448
+constexpr int kTopK = DSA_TOPK;
+constexpr int kBins = 4096;                     // 12-bit radix digit
+constexpr uint32_t kZeroKey = 0x80000000u;      // key of +0.0 (and of masked-out tokens)
+constexpr int kZeroBin = static_cast<int>(kZeroKey >> 20);
+constexpr int kHistWsPerRow = 2 * kBins + 2;    // [ghist1 | ghist2 | (positives, zeros)]
+
+// ------------------------------------------------------------------------------------------
+// Order-preserving float -> uint32 key (sparse_mask_topk.cu:40-43): larger float, larger key;
+// -0.0 sorts just below +0.0.
+__device__ __forceinline__ uint32_t float_key(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// fp32 -> bf16, round to nearest even, NaN -> 0x7FC0 (the c10::BFloat16 conversion).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (f != f) ? 0x7FC0u : r;
+}
+
+// fp32 -> OCP fp8 e4m3fn (bias 7, max 448, no infinities), round to nearest even, not
+// saturating: |x| > 464 (which rounds past 448; 464 itself ties to the even 448), infinities and
+// NaN give 0x7F | sign -- the behaviour of torch's float -> float8_e4m3fn cast.  Written from
+// the format definition.
+__device__ __forceinline__ uint32_t fp8_e4m3_rne(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  uint32_t code;
+  if (a > 0x43E80000u) {                  // above 464.0f, +inf, NaN
+    code = 0x7Fu;
+  } else if (a < 0x3C800000u) {           // below 2^-6: subnormal grid of 2^-9
+    code = static_cast<uint32_t>(rintf(__uint_as_float(a) * 512.0f));
+  } else {                                // normal: keep 3 mantissa bits, RNE on the other 20
+    const uint32_t t = a + 0x7FFFFu + ((a >> 20) & 1u);
+    code = (t >> 20) - (120u << 3);
+  }
+  return code | sign;
+}
+
+// OCP fp8 e4m3fn -> fp32, exact (software; used where the throughput does not matter).
+__device__ __forceinline__ float fp8_e4m3_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 0xFu;
+  const uint32_t m = b & 7u;
+  float v;
+  if (e == 0) v = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  else if (e == 15 && m == 7) v = __uint_as_float(0x7FC00000u);
+  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (b & 0x80u) ? -v : v;
+}
+
+// ------------------------------------------------------------------------------------------
+// Wave helpers (wave64).
+__device__ __forceinline__ int lane_id() { return static_cast<int>(__lane_id()); }
+
+// Number of set bits of `mask` in lanes below this one.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// Exclusive prefix (lane order) and wave total of per-lane counts in [0, 7]: three ballots.
+__device__ __forceinline__ int wave_prefix_small(int c, int& total) {
+  const uint64_t b0 = __ballot(c & 1);
+  const uint64_t b1 = __ballot(c & 2);
+  const uint64_t b2 = __ballot(c & 4);
+  total = __popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2);
+  return lanes_below(b0) + 2 * lanes_below(b1) + 4 * lanes_below(b2);
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+}  // namespace dsa
+
+// ------------------------------------------------------------------------------------------
+// Host-side status plumbing (defined in status.cpp).
+namespace dsa {
+int fail(int code, const char* fmt, ...);
+int ok();
+int check_launch(const char* what);
+}  // namespace dsa
+
+#define DSA_REQUIRE(cond, ...)                                      \
+  do {                                                              \
+    if (!(cond)) return ::dsa::fail(DSA_ERR_INVALID, __VA_ARGS__);  \
+  } while (0)

@@ -1,0 +1,367 @@
+// Paged MQA indexer logits for decode on gfx950 fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4).
+//
+//   logits[r, t] = scale[t] * sum_h w[r, h] * relu(q8[r, h, :] . k8[t, :])
+//   mask[r, t/16] bit t%16 = t < len[r] && bits(logits[r, t]) != 0
+//
+// Semantics follow hcu_ops/csrc/mqa_hist.cu:96-273 (rows of a request group share the first
+// row's block table, the K scale is applied after the weighted ReLU sum, mask bit = kept and
+// nonzero); the work decomposition is this file's own:
+//
+//  * One MFMA computes a [16 heads x 16 tokens] tile with the whole 128-deep contraction.  The
+//    A operand is q (heads), held in VGPRs for the life of the wave: lane l holds head
+//    tile*16 + l%16, bytes (l/16)*32 .. +32.  The B operand is 16 tokens of a K page loaded
+//    straight from HBM with the same byte mapping (2 x 16 B per lane, 2 KB contiguous per wave),
+//    so the instruction's K ordering is the same permutation on both sides and cancels.
+//  * Result lane l holds heads 4*(l/16)+i of token l%16: the epilogue is an in-lane
+//    max/fma chain over H/4 values, two xor-shuffles (16, 32), and a lane select that leaves
+//    lane l with token l of the page.  One 256 B logits store and one K-scale load per page.
+//  * Each CTA (4 waves) owns `ppc` consecutive pages of one row group (R rows of a request);
+//    wave w takes pages w, w+4, ... and prefetches its next page while computing the current.
+//    Grid = chunks x row groups, row groups fastest.  CTAs whose pages lie past the rows'
+//    lengths only zero their mask words, so no separate mask memset is launched.
+//  * kHist: also the top-k pass-1 histogram (12-bit key[31:20] of the nonzero logits of rows
+//    with min(hist_len, width) > 2048, plus positive / zero counts), as LDS counts flushed with
+//    one global atomic per nonzero bin; mqa_hist_init_kernel seeds the zero bin / zero count
+//    with the row length (mqa_hist.cu:278-304) and every CTA subtracts its nonzero tokens.
+#include "dsa_common.h"
+
+namespace dsa {
+namespace {
+
+using i32x8 = __attribute__((ext_vector_type(8))) int;
+using f32x4 = __attribute__((ext_vector_type(4))) float;
+using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerCta = kThreads / kWave;
+
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
+  // scale operands 0 select the unscaled v_mfma_f32_16x16x128_f8f6f4 (both operands fp8 e4m3)
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// 32 bytes at p (16-B aligned) as an MFMA operand.
+__device__ __forceinline__ i32x8 load_frag(const uint8_t* p) {
+  const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 b = *reinterpret_cast<const u32x4*>(p + 16);
+  return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+}
+
+__device__ __forceinline__ i32x8 load_frag_nt(const uint8_t* p) {
+  const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 16));
+  return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+}
+
+struct PageRegs {
+  i32x8 k[4];  // 4 sub-tiles of 16 tokens
+  float scale; // scale of token lane_id() of the page
+};
+
+__device__ __forceinline__ void load_page(const uint8_t* __restrict__ kv, int64_t page_stride, int phys, int lane,
+                                          PageRegs& pr) {
+  const uint8_t* page = kv + static_cast<int64_t>(phys) * page_stride;
+  const uint8_t* p = page + (lane & 15) * kHeadDim + (lane >> 4) * 32;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) pr.k[st] = load_frag_nt(p + st * 16 * kHeadDim);
+  pr.scale = __builtin_nontemporal_load(reinterpret_cast<const float*>(page + kPageFp8Bytes) + lane);
+}
+
+struct DecodeArgs {
+  const uint8_t* q8;
+  const float* w;
+  const uint8_t* kv;
+  int64_t page_stride;
+  const int32_t* ctx;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int bt_pages;
+  int width;
+  float* logits;
+  int64_t logits_stride;
+  int16_t* mask;
+  int64_t mask_stride;
+  int group;
+  int n_rowgroups;  // batch / R
+  int ppc;          // pages per CTA
+  const int32_t* hist_lens;
+  int32_t* hist_ws;
+  int64_t batch;
+};
+
+template <int H, int R, bool kHist>
+__global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const DecodeArgs a) {
+  constexpr int HT = H / 16;  // head tiles
+  extern __shared__ int s_hist[];  // kHist: [R][kBins]
+  __shared__ int s_cnt[2 * R];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rg = static_cast<int>(blockIdx.x % static_cast<uint32_t>(a.n_rowgroups));
+  const int chunk = static_cast<int>(blockIdx.x / static_cast<uint32_t>(a.n_rowgroups));
+  const int row0 = rg * R;
+  const int group_row = (row0 / a.group) * a.group;
+
+  int len[R];
+  int hlim[R];
+  int max_len = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int l = a.ctx[row0 + r];
+    len[r] = l < 0 ? 0 : (l > a.width ? a.width : l);
+    max_len = len[r] > max_len ? len[r] : max_len;
+    hlim[r] = 0;
+    if constexpr (kHist) {
+      int h = a.hist_lens[row0 + r];
+      h = h < a.width ? h : a.width;
+      hlim[r] = h > kTopK ? h : 0;
+    }
+  }
+  const int n_pages = (max_len + kPage - 1) / kPage;
+  const int p_begin = chunk * a.ppc;
+  const int p_end = min(p_begin + a.ppc, a.bt_pages);
+  const int p_live = min(p_end, n_pages);
+
+  // Mask words of pages past every row's length: zero them (4 words per page and row).
+  for (int p0 = max(p_begin, n_pages); p0 < p_end; p0 += kThreads / 4) {
+    const int p = p0 + (tid >> 2);
+    if (p < p_end) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) a.mask[static_cast<int64_t>(row0 + r) * a.mask_stride + p * 4 + (tid & 3)] = 0;
+    }
+  }
+  if (p_begin >= p_live) return;  // uniform over the CTA, before any barrier
+
+  if constexpr (kHist) {
+    for (int i = tid; i < R * kBins; i += kThreads) s_hist[i] = 0;
+    if (tid < 2 * R) s_cnt[tid] = 0;
+    __syncthreads();
+  }
+
+  // q / w fragments (see header comment for the lane mapping).
+  i32x8 qf[R][HT];
+  float wf[R][HT * 4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint8_t* qr = a.q8 + static_cast<int64_t>(row0 + r) * H * kHeadDim + (lane & 15) * kHeadDim + (lane >> 4) * 32;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) qf[r][ht] = load_frag(qr + ht * 16 * kHeadDim);
+    const float* wr = a.w + static_cast<int64_t>(row0 + r) * H + 4 * (lane >> 4);
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wf[r][ht * 4 + i] = wr[ht * 16 + i];
+    }
+  }
+
+  const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride;
+  int nz[R], pos[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) nz[r] = pos[r] = 0;
+
+  int p = p_begin + wave;
+  if (p < p_live) {
+    PageRegs cur;
+    load_page(a.kv, a.page_stride, uniform(btr[p]), lane, cur);
+    while (true) {
+      const int pn = p + kWavesPerCta;
+      PageRegs nxt;
+      // Branch-free prefetch: past the end the current page is loaded again.
+      load_page(a.kv, a.page_stride, uniform(btr[pn < p_live ? pn : p]), lane, nxt);
+
+      float val[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) val[r] = 0.0f;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          f32x4 acc[HT];
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma_fp8(qf[r][ht], cur.k[st], f32x4{0.f, 0.f, 0.f, 0.f});
+          float s = 0.0f;
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s += fmaxf(acc[ht][i], 0.0f) * wf[r][ht * 4 + i];
+          }
+          s += __shfl_xor(s, 16);
+          s += __shfl_xor(s, 32);
+          val[r] = (lane >> 4) == st ? s : val[r];
+        }
+      }
+
+      const int token = p * kPage + lane;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float v = val[r] * cur.scale;
+        const bool live = token < len[r];
+        const bool keep = live && __float_as_uint(v) != 0u;
+        const uint64_t bits = __ballot(keep);
+        const int64_t row = row0 + r;
+        if (lane < 4) a.mask[row * a.mask_stride + p * 4 + lane] = static_cast<int16_t>((bits >> (16 * lane)) & 0xFFFFu);
+        if (live) a.logits[row * a.logits_stride + token] = v;
+        if constexpr (kHist) {
+          if (keep && token < hlim[r]) {
+            const uint32_t key = float_key(v);
+            atomicAdd(&s_hist[r * kBins + static_cast<int>(key >> 20)], 1);
+            ++nz[r];
+            pos[r] += key > kZeroKey;
+          }
+        }
+      }
+
+      p = pn;
+      if (p >= p_live) break;
+      cur = nxt;
+    }
+  }
+
+  if constexpr (kHist) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = wave_sum(nz[r]);
+      const int q = wave_sum(pos[r]);
+      if (lane == 0 && n) {
+        atomicAdd(&s_cnt[2 * r], n);
+        atomicAdd(&s_cnt[2 * r + 1], q);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (hlim[r] == 0) continue;
+      int32_t* gh = a.hist_ws + static_cast<int64_t>(row0 + r) * kBins;
+      int32_t* gcnt = a.hist_ws + 2 * a.batch * kBins + 2 * static_cast<int64_t>(row0 + r);
+      for (int i = tid; i < kBins; i += kThreads) {
+        const int c = s_hist[r * kBins + i];
+        if (c) atomicAdd(&gh[i], c);
+      }
+      if (tid == 0) {
+        const int n = s_cnt[2 * r];
+        const int q = s_cnt[2 * r + 1];
+        if (n) {
+          atomicSub(&gh[kZeroBin], n);
+          atomicSub(&gcnt[1], n);
+        }
+        if (q) atomicAdd(&gcnt[0], q);
+      }
+    }
+  }
+}
+
+// Seeds the top-k pass-1 workspace: every token below min(hist_len, width) counts as a zero
+// until the logits kernel subtracts its nonzero ones.  Rows with <= 2048 tokens stay empty.
+__global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __restrict__ hist_lens, int width,
+                                                            int64_t batch, int32_t* __restrict__ ws) {
+  const int64_t row = blockIdx.x;
+  int h = hist_lens[row];
+  h = h < width ? h : width;
+  const int zeros = h > kTopK ? h : 0;
+  int32_t* g1 = ws + row * kBins;
+  int32_t* g2 = ws + (batch + row) * kBins;
+  for (int i = threadIdx.x; i < kBins; i += 256) {
+    g1[i] = i == kZeroBin ? zeros : 0;
+    g2[i] = 0;
+  }
+  if (threadIdx.x == 0) {
+    int32_t* c = ws + 2 * batch * kBins + 2 * row;
+    c[0] = 0;
+    c[1] = zeros;
+  }
+}
+
+template <int H, int R, bool kHist>
+void launch_one(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
+  const size_t lds = kHist ? static_cast<size_t>(R) * kBins * sizeof(int) : 0;
+  hipLaunchKernelGGL((mqa_logits_decode_kernel<H, R, kHist>), dim3(grid), dim3(kThreads), lds, stream, a);
+}
+
+template <int H, bool kHist>
+void launch_r(const DecodeArgs& a, int R, uint32_t grid, hipStream_t stream) {
+  switch (R) {
+    case 1: launch_one<H, 1, kHist>(a, grid, stream); break;
+    case 2: launch_one<H, 2, kHist>(a, grid, stream); break;
+    case 3: launch_one<H, 3, kHist>(a, grid, stream); break;
+    default:
+      if constexpr (!kHist) launch_one<H, 4, false>(a, grid, stream);
+      break;
+  }
+}
+
+}  // namespace
+}  // namespace dsa
+
+using namespace dsa;
+
+extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t batch, int group_size,
+                                     const uint8_t* kv_cache, int64_t page_stride_bytes,
+                                     const int32_t* context_lens, const int32_t* block_table, int64_t bt_stride,
+                                     int64_t bt_pages, float* logits, int64_t logits_stride, int16_t* mask,
+                                     int64_t mask_stride, int rows_per_cta, int pages_per_cta,
+                                     const int32_t* hist_lens, int32_t* hist_ws, hipStream_t stream) {
+  DSA_REQUIRE(heads == 32 || heads == 64, "dsa_mqa_logits_decode: heads must be 32 or 64 (got %d)", heads);
+  DSA_REQUIRE(batch >= 0 && group_size >= 1, "dsa_mqa_logits_decode: batch must be >= 0 and group_size >= 1");
+  DSA_REQUIRE(batch % group_size == 0, "dsa_mqa_logits_decode: batch must be a multiple of group_size");
+  if (rows_per_cta <= 0) rows_per_cta = group_size % 2 == 0 ? 2 : 1;
+  DSA_REQUIRE(rows_per_cta >= 1 && rows_per_cta <= 4 && group_size % rows_per_cta == 0,
+              "dsa_mqa_logits_decode: rows_per_cta must be in 1..4 and divide group_size");
+  DSA_REQUIRE(bt_pages > 0 && bt_pages * kPage <= 0x7FFFFFFF,
+              "dsa_mqa_logits_decode: block table capacity must be positive and below 2^31 tokens");
+  if (batch == 0) return ok();
+  DSA_REQUIRE(q8 && w && kv_cache && context_lens && block_table && logits && mask,
+              "dsa_mqa_logits_decode: null pointer");
+  DSA_REQUIRE(page_stride_bytes >= kPageBytes && page_stride_bytes % 16 == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv_cache) & 15u) == 0,
+              "dsa_mqa_logits_decode: kv_cache pages must be >= 8448 B with a 16-B aligned stride");
+  DSA_REQUIRE((reinterpret_cast<uintptr_t>(q8) & 15u) == 0, "dsa_mqa_logits_decode: q8 must be 16-B aligned");
+  const int64_t width = bt_pages * kPage;
+  DSA_REQUIRE(bt_stride >= bt_pages && logits_stride >= width && mask_stride >= width / 16,
+              "dsa_mqa_logits_decode: strides smaller than the block table capacity");
+  DSA_REQUIRE((hist_lens == nullptr) == (hist_ws == nullptr),
+              "dsa_mqa_logits_decode: hist_lens and hist_ws go together");
+  if (pages_per_cta <= 0) pages_per_cta = 8;
+  DSA_REQUIRE(pages_per_cta <= 4096, "dsa_mqa_logits_decode: pages_per_cta too large");
+  const bool hist = hist_ws != nullptr;  // 32-bit LDS counters: no limit on tokens per CTA
+  DSA_REQUIRE(!hist || rows_per_cta <= 3,
+              "dsa_mqa_logits_decode: the fused histogram needs rows_per_cta <= 3 (16 KB of LDS per row)");
+
+  DecodeArgs a;
+  a.q8 = q8;
+  a.w = w;
+  a.kv = kv_cache;
+  a.page_stride = page_stride_bytes;
+  a.ctx = context_lens;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.bt_pages = static_cast<int>(bt_pages);
+  a.width = static_cast<int>(width);
+  a.logits = logits;
+  a.logits_stride = logits_stride;
+  a.mask = mask;
+  a.mask_stride = mask_stride;
+  a.group = group_size;
+  a.n_rowgroups = static_cast<int>(batch / rows_per_cta);
+  a.ppc = pages_per_cta;
+  a.hist_lens = hist_lens;
+  a.hist_ws = hist_ws;
+  a.batch = batch;
+  const int64_t chunks = (bt_pages + pages_per_cta - 1) / pages_per_cta;
+  const int64_t grid = chunks * a.n_rowgroups;
+  DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_mqa_logits_decode: grid too large");
+
+  if (hist) {
+    hipLaunchKernelGGL(mqa_hist_init_kernel, dim3(static_cast<uint32_t>(batch)), dim3(256), 0, stream, hist_lens,
+                       a.width, batch, hist_ws);
+  }
+  const uint32_t g = static_cast<uint32_t>(grid);
+  if (heads == 64) {
+    if (hist) launch_r<64, true>(a, rows_per_cta, g, stream);
+    else launch_r<64, false>(a, rows_per_cta, g, stream);
+  } else {
+    if (hist) launch_r<32, true>(a, rows_per_cta, g, stream);
+    else launch_r<32, false>(a, rows_per_cta, g, stream);
+  }
+  return check_launch("dsa_mqa_logits_decode");
+}

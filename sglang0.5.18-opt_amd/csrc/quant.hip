@@ -1,0 +1,104 @@
+// Per-vector fp8 quantisation for the indexer: q (per row and head) and the K-cache writer
+// (per token, into the 132-B paged layout).  Convention (hcu_ops/csrc/norm_quant.cu:13-14,
+// applied per 128-element vector): amax = max|x|, scale = amax / 448,
+// q = fp8_rne(x * (448 / amax)), with amax == 0 giving q = 0 and scale = 0.
+// 16 lanes own one 128-element vector (8 bf16 = 16 B each); a wave handles 4 vectors.
+#include "dsa_common.h"
+
+namespace dsa {
+namespace {
+
+using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
+
+constexpr int kQThreads = 256;
+constexpr int kVecPerCta = kQThreads / 16;
+
+// Loads this lane's 8 bf16 of a vector, returns the vector's amax (all 16 lanes agree) and
+// the 8 fp8 codes packed into two words.
+__device__ __forceinline__ float quant_vec(const uint16_t* src, int sub, u32x2& packed, float& scale) {
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(src + sub * 8);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(raw[i] << 16);
+    x[2 * i + 1] = __uint_as_float(raw[i] & 0xFFFF0000u);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const float inv = amax == 0.0f ? 0.0f : 448.0f / amax;
+  scale = amax / 448.0f;
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = fp8_e4m3_rne(x[i] * inv);
+  packed = u32x2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24), c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
+  return amax;
+}
+
+__global__ __launch_bounds__(kQThreads) void quant_q_kernel(const uint16_t* __restrict__ q, const float* __restrict__ w,
+                                                            int64_t n_vec, uint8_t* __restrict__ q8,
+                                                            float* __restrict__ w_eff) {
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * kVecPerCta + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (v >= n_vec) return;  // whole 16-lane groups drop out together
+  u32x2 packed;
+  float scale;
+  quant_vec(q + v * kHeadDim, sub, packed, scale);
+  *reinterpret_cast<u32x2*>(q8 + v * kHeadDim + sub * 8) = packed;
+  if (sub == 0) w_eff[v] = w[v] * scale;
+}
+
+__global__ __launch_bounds__(kQThreads) void store_k_kernel(const uint16_t* __restrict__ k, int64_t n,
+                                                            const int32_t* __restrict__ slots,
+                                                            uint8_t* __restrict__ kv, int64_t page_stride) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kVecPerCta + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (t >= n) return;
+  const int32_t slot = slots[t];
+  if (slot < 0) return;  // padded entries are not stored
+  u32x2 packed;
+  float scale;
+  quant_vec(k + t * kHeadDim, sub, packed, scale);
+  uint8_t* page = kv + static_cast<int64_t>(slot >> 6) * page_stride;
+  const int off = slot & (kPage - 1);
+  *reinterpret_cast<u32x2*>(page + off * kHeadDim + sub * 8) = packed;
+  if (sub == 0) *reinterpret_cast<float*>(page + kPageFp8Bytes + off * 4) = scale;
+}
+
+}  // namespace
+}  // namespace dsa
+
+using namespace dsa;
+
+extern "C" int dsa_quant_q_fp8(const uint16_t* q_bf16, const float* w, int64_t rows, int heads, uint8_t* q8,
+                               float* w_eff, hipStream_t stream) {
+  DSA_REQUIRE(rows >= 0 && heads > 0, "dsa_quant_q_fp8: rows must be >= 0 and heads > 0");
+  const int64_t n_vec = rows * heads;
+  if (n_vec == 0) return ok();
+  DSA_REQUIRE(q_bf16 && w && q8 && w_eff, "dsa_quant_q_fp8: null pointer");
+  DSA_REQUIRE((reinterpret_cast<uintptr_t>(q_bf16) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q8) & 7u) == 0,
+              "dsa_quant_q_fp8: q must be 16-B aligned and q8 8-B aligned");
+  const int64_t grid = (n_vec + kVecPerCta - 1) / kVecPerCta;
+  DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_quant_q_fp8: too many rows");
+  hipLaunchKernelGGL(quant_q_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kQThreads), 0, stream, q_bf16, w, n_vec,
+                     q8, w_eff);
+  return check_launch("dsa_quant_q_fp8");
+}
+
+extern "C" int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* slots, uint8_t* kv_cache,
+                                 int64_t page_stride_bytes, hipStream_t stream) {
+  DSA_REQUIRE(n_tokens >= 0, "dsa_store_k_cache: n_tokens must be >= 0");
+  if (n_tokens == 0) return ok();
+  DSA_REQUIRE(k_bf16 && slots && kv_cache, "dsa_store_k_cache: null pointer");
+  DSA_REQUIRE(page_stride_bytes >= kPageBytes && page_stride_bytes % 16 == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv_cache) & 15u) == 0 && (reinterpret_cast<uintptr_t>(k_bf16) & 15u) == 0,
+              "dsa_store_k_cache: pages must be >= 8448 B and 16-B aligned; k must be 16-B aligned");
+  const int64_t grid = (n_tokens + kVecPerCta - 1) / kVecPerCta;
+  DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_store_k_cache: too many tokens");
+  hipLaunchKernelGGL(store_k_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kQThreads), 0, stream, k_bf16, n_tokens,
+                     slots, kv_cache, page_stride_bytes);
+  return check_launch("dsa_store_k_cache");
+}

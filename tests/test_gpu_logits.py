@@ -1,0 +1,108 @@
+"""GPU parity of the MQA indexer logits (decode and prefill) against the oracle:
+logits within the documented tolerance (tests/gpu_util.py), the 16-token nonzero mask and the
+fused top-k pass-1 histogram bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import hcu_ops
+from hcu_ops import workloads as wl
+from oracle import indexer as O
+
+from gpu_util import check_logits, kv_np, oracle_decode, oracle_q
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_decode(case, gpu, pctas=0, rpc=None, hist=False):
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    lens = case.context_lens.to(gpu)
+    lg, mask = hcu_ops.mqa_logits(q8.unsqueeze(1), case.kv.to(gpu), w, lens, case.block_table.to(gpu), case.width,
+                                  case.group, hist_lens=lens if hist else None, persistent_ctas=pctas,
+                                  rows_per_cta=rpc)
+    return q8, w, lg, mask
+
+
+def _check_decode(case, lg, mask):
+    q8, w = oracle_q(case)
+    ref, mag, ref_mask = oracle_decode(case, q8, w)
+    got_mask = mask.cpu().numpy()
+    assert np.array_equal(got_mask, ref_mask), "nonzero mask differs"
+    got = lg.cpu().numpy()
+    for r in range(case.rows):
+        L = int(case.context_lens[r])
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
+
+
+@pytest.mark.parametrize("heads", [64, 32])
+@pytest.mark.parametrize("group,lens,rpc", [
+    (1, [4096], 1),
+    (1, [5000, 130, 64, 65, 2049], 1),
+    (2, [3000, 7000, 1], 1),
+    (2, [3000, 7000, 1], 2),
+    (6, [2500, 900], 1),
+    (6, [2500, 900], 2),
+    (6, [2500, 900], 3),
+    (4, [1000, 1200], 4),
+])
+def test_decode_logits(gpu, heads, group, lens, rpc):
+    case = wl.decode_case(100 + len(lens) + group, lens, group=group, heads=heads,
+                          bt_pages=max((L + group + 63) // 64 for L in lens) + 3)
+    _, _, lg, mask = _run_decode(case, gpu, rpc=rpc)
+    _check_decode(case, lg, mask)
+
+
+@pytest.mark.parametrize("pctas", [1, 3, 64, 1000])
+def test_decode_logits_cta_split(gpu, pctas):
+    case = wl.decode_case(7, [9000, 4000], group=2, heads=64)
+    _, _, lg, mask = _run_decode(case, gpu, pctas=pctas, rpc=2)
+    _check_decode(case, lg, mask)
+
+
+def test_decode_logits_sparse_and_negative_modes(gpu):
+    """The reference's 'sparse' and 'neg' modes (test_mqa_hist.py:31-49): all-negative dot
+    products give exact zeros (mask bit clear), all-negative weights give negative logits."""
+    case = wl.decode_case(9, [3000, 2500], group=1, heads=64)
+    kvf = case.kv.view(case.kv.shape[0], -1).clone()
+    codes = kvf[:, :8192].view(-1, 128)
+    vals = codes.view(torch.float8_e4m3fn).float().abs()
+    g = torch.Generator().manual_seed(1)
+    pos = torch.rand(codes.shape[0], 1, generator=g) < 0.05
+    codes.copy_(torch.where(pos, vals, -vals).to(torch.float8_e4m3fn).view(torch.uint8))
+    case.kv = kvf.view(case.kv.shape)
+    case.q = case.q.abs()
+    case.w = case.w.abs()
+    _, _, lg, mask = _run_decode(case, gpu)
+    _check_decode(case, lg, mask)
+    bits = O.unpack_mask(mask.cpu().numpy(), case.width)
+    assert 0 < bits.sum() < 0.2 * case.context_lens.sum()
+    case.w = -case.w
+    _, _, lg, mask = _run_decode(case, gpu)
+    _check_decode(case, lg, mask)
+
+
+@pytest.mark.parametrize("group,lens", [(1, [9000, 5000, 1500, 40000]), (2, [20000, 3000])])
+def test_decode_fused_histogram(gpu, group, lens):
+    case = wl.decode_case(13, lens, group=group, heads=64)
+    _, _, lg, mask = _run_decode(case, gpu, hist=True)
+    zws = hcu_ops._MQA_HIST[2].cpu().numpy() if hcu_ops._MQA_HIST is not None else None
+    assert zws is not None, "fused histogram not requested"
+    lens_np = case.context_lens.numpy()
+    ref = O.pass1_hist(lg.cpu().numpy(), mask.cpu().numpy(), lens_np, case.width)
+    assert np.array_equal(zws, ref)
+    _check_decode(case, lg, mask)
+
+
+@pytest.mark.parametrize("heads,n_q,prefix", [(64, 40, 3000), (32, 9, 130), (64, 17, 0)])
+def test_prefill_logits(gpu, heads, n_q, prefix):
+    case = wl.prefill_case(21 + n_q, n_q, prefix, heads=heads)
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    width = case.n_keys + 5
+    bt = torch.cat([case.block_table, torch.zeros(1, dtype=torch.int32)])  # capacity for width
+    lg = hcu_ops.mqa_logits_prefill(q8, w, case.kv.to(gpu), bt.to(gpu), case.lens.to(gpu), width)
+    rq8, rw = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
+    ref, mag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), bt.numpy(), case.lens.numpy(), width)
+    got = lg.cpu().numpy()
+    for r in range(case.rows):
+        L = int(case.lens[r])
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")

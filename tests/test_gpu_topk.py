@@ -1,0 +1,106 @@
+"""GPU parity of the exact top-2048 + page-table transform: the selected sets (rows compared
+sorted) equal the oracle's on the same scores, for the reference's ten score distributions
+(hcu_ops/tests/topk_lib.py:8-51), ragged / padded rows, the 1M-wide production layout, every
+split count, the fused pass-1 path and the varlen layout."""
+import numpy as np
+import pytest
+import torch
+
+import hcu_ops
+from hcu_ops import _C
+from hcu_ops import workloads as wl
+from oracle import indexer as O
+from oracle.topk_c import topk_radix
+
+from gpu_util import sorted_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(x, mask, lengths, pt, W, cu=None):
+    return topk_radix(x.numpy(), None if mask is None else mask.numpy(), lengths.numpy(), pt.numpy(), W,
+                      cu_seqlens_q=None if cu is None else cu.numpy())
+
+
+IMPLS = {
+    "single": lambda x, m, l, p, c: _C.sparse_mask_topk_transform(x, m, l, p, c, 2048),
+    "s2": lambda x, m, l, p, c: _C.sparse_mask_topk_transform_split(x, m, l, p, c, 2048, 2),
+    "s8": lambda x, m, l, p, c: _C.sparse_mask_topk_transform_split(x, m, l, p, c, 2048, 8),
+    "s16": lambda x, m, l, p, c: _C.sparse_mask_topk_transform_split(x, m, l, p, c, 2048, 16),
+}
+
+
+@pytest.mark.parametrize("dist", wl.TOPK_DISTS)
+@pytest.mark.parametrize("B", [6, 24])
+def test_topk_distributions(gpu, dist, B):
+    for L in [1000, 2048, 2049, 4096, 16384, 65536]:
+        for ragged in [False, True]:
+            W = 2 * L + 64 if ragged and L >= 16384 else L + 64
+            x, mask, lengths, pt = wl.topk_scores(B, L, dist, W=W, ragged=ragged, seed=L + B)
+            ref = sorted_rows(_oracle(x, mask, lengths, pt, W))
+            xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
+            cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
+            for name, fn in IMPLS.items():
+                got = sorted_rows(fn(xg, mg, lg, pg, cu).cpu().numpy())
+                assert np.array_equal(got, ref), f"{dist} B={B} L={L} ragged={ragged} impl={name}"
+
+
+@pytest.mark.parametrize("dist", ["relu_sum", "narrow", "sparse2"])
+def test_topk_production_width(gpu, dist):
+    """Score width = page-table capacity (1M) with ragged rows of 16K..128K tokens."""
+    for L in [16384, 131072]:
+        x, mask, lengths, pt = wl.topk_scores(6, L, dist, W=1 << 20, ragged=True, seed=L)
+        ref = sorted_rows(_oracle(x, mask, lengths, pt, 1 << 20))
+        xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
+        cu = torch.arange(7, dtype=torch.int32, device=gpu)
+        for name, fn in IMPLS.items():
+            got = sorted_rows(fn(xg, mg, lg, pg, cu).cpu().numpy())
+            assert np.array_equal(got, ref), f"W1M {dist} L={L} impl={name}"
+        del xg, mg, pg
+
+
+def test_topk_many_rows_and_empty(gpu):
+    x, mask, lengths, pt = wl.topk_scores(600, 5000, "relu_sum", W=5056, ragged=True, seed=1)
+    ref = sorted_rows(_oracle(x, mask, lengths, pt, 5056))
+    out = hcu_ops.sparse_mask_topk_transform(x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu),
+                                             torch.arange(601, dtype=torch.int32, device=gpu))
+    assert np.array_equal(sorted_rows(out.cpu().numpy()), ref)
+    e = torch.empty(0, 4096, device=gpu)
+    out = hcu_ops.sparse_mask_topk_transform(e, torch.empty(0, 256, dtype=torch.int16, device=gpu),
+                                             torch.empty(0, dtype=torch.int32, device=gpu),
+                                             torch.empty(0, 4096, dtype=torch.int32, device=gpu),
+                                             torch.zeros(1, dtype=torch.int32, device=gpu))
+    assert tuple(out.shape) == (0, 2048)
+
+
+def test_topk_dense_and_varlen(gpu):
+    """Dense scores (no mask) with the varlen layout: rows map to their request's page table."""
+    x, _, lengths, _ = wl.topk_scores(7, 9000, "mixed", seed=5)
+    lengths = torch.tensor([9000, 3000, 2048, 2049, 8999, 100, 6000], dtype=torch.int32)
+    cu = torch.tensor([0, 3, 4, 7], dtype=torch.int32)
+    pt = (torch.arange(9000, dtype=torch.int32)[None, :] + 100000 * torch.arange(3, dtype=torch.int32)[:, None])
+    ref = sorted_rows(_oracle(x, None, lengths, pt, 9000, cu=cu))
+    for splits in [1, 4]:
+        got = hcu_ops.topk_transform(x.to(gpu), lengths.to(gpu), pt.contiguous().to(gpu), cu.to(gpu),
+                                     max_splits=splits)
+        assert np.array_equal(sorted_rows(got.cpu().numpy()), ref), f"splits={splits}"
+
+
+def test_topk_fused_pass1_pairing(gpu):
+    """mqa_logits(hist_lens=lengths) -> sparse_mask_topk_transform consumes the fused pass 1 and
+    gives the same set as the top-k with its own pass 1 on the same logits."""
+    case = wl.decode_case(17, [30000, 12000, 4000, 1000], group=1, heads=64)
+    gl = lambda t: t.to(gpu)
+    q8, w = hcu_ops.quant_q_fp8(gl(case.q), gl(case.w))
+    lens = gl(case.context_lens)
+    pt = gl(case.page_table_1())
+    cu = torch.arange(case.rows + 1, dtype=torch.int32, device=gpu)
+    lg, mask = hcu_ops.mqa_logits(q8.unsqueeze(1), gl(case.kv), w, lens, gl(case.block_table), case.width, 1,
+                                  hist_lens=lens)
+    assert hcu_ops._MQA_HIST is not None
+    fused = hcu_ops.sparse_mask_topk_transform(lg, mask, lens, pt, cu)
+    assert hcu_ops._MQA_HIST is None
+    plain = _C.sparse_mask_topk_transform(lg, mask, lens, pt, cu, 2048)
+    ref = _oracle(lg.cpu(), mask.cpu(), case.context_lens, case.page_table_1(), case.width)
+    assert np.array_equal(sorted_rows(fused.cpu().numpy()), sorted_rows(ref))
+    assert np.array_equal(sorted_rows(plain.cpu().numpy()), sorted_rows(ref))
