@@ -1,0 +1,368 @@
+"""Benchmark of the MI355X DSA indexer path (one GPU).
+
+A step is one pass of the indexer over one batch with every input resident in HBM:
+  decode   bf16 q -> fp8 quant -> paged fp8 MQA logits (+ fused top-k pass 1) -> top-2048 +
+           page-table remap
+  prefill  paged K dequant to bf16 -> q quant -> causal fp8 MQA logits -> top-2048 + remap
+The step is captured once in a hipGraph and replayed; W replays warm up, K replays are timed
+between two synchronisations.  value = indexer K-tokens scored per second (tokens scored =
+sum over query rows of the keys that row scores).
+
+The JSON line also carries
+  roofline      the dominant kernel (the logits kernel) timed live with HIP events on its launch
+                stream over graph replays of that kernel alone, against its algorithmic bytes
+                (decode: HBM) or flops (prefill: fp8 MFMA);
+  path_roofline the whole step's algorithmic bytes / flops against the same peak;
+  cpu_baseline  the oracle's torch-CPU restatement (dequant -> fp32 matmul -> relu*w -> sum ->
+                *scale -> kthvalue top-2048 -> gather) timed on a bounded sample of the same
+                workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_mtp64]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sglang0.5.18-opt_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA
+METRIC = "indexer K-tokens scored/sec (logits+top2048) at 64K ctx"
+
+WORKLOADS = {
+    "decode_1x4k": "decode, 1 request x 1 row, 4096-token paged fp8 K, 64 heads x 128",
+    "decode_32x16k": "decode, 32 requests x 1 row, 16384 tokens each, 64 heads x 128, fp8 paged K (page 64)",
+    "decode_mtp64": "decode MTP verify, 64 requests x 2 rows, ctx U[2048, 65536], 64 heads x 128, "
+                    "fp8 paged K (page 64), shuffled pages",
+    "prefill_8k_64k": "chunked prefill, 8192 query rows over a 65536-token cached prefix (73728 keys, causal), "
+                      "64 heads x 128",
+    "prefill_16k_128k": "long prefill, 16384 query rows over 147456 keys (causal) in 4096-row slabs, "
+                        "Student-t(4) K, 64 heads x 128",
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+# ---------------------------------------------------------------------------------------------
+# Decode
+
+class DecodeStep:
+    def __init__(self, case, dev):
+        import torch
+        import hcu_ops
+        self.h = hcu_ops
+        self.case = case
+        g = lambda t: t.to(dev)
+        self.q, self.w, self.kv = g(case.q), g(case.w), g(case.kv)
+        self.lens, self.bt = g(case.context_lens), g(case.block_table)
+        self.pt = g(case.page_table_1())
+        self.cu = torch.arange(case.rows + 1, dtype=torch.int32, device=dev)
+        self.out = None
+
+    def __call__(self):
+        h, c = self.h, self.case
+        q8, w = h.quant_q_fp8(self.q, self.w)
+        logits, mask = h.mqa_logits(q8.unsqueeze(1), self.kv, w, self.lens, self.bt, c.width, c.group,
+                                    hist_lens=self.lens)
+        self.out = h.sparse_mask_topk_transform(logits, mask, self.lens, self.pt, self.cu)
+        return self.out
+
+    def logits_only(self, hist=False):
+        """The dominant kernel alone (the step's launch shape, q already quantised); hist=True adds
+        the fused top-k pass 1 and its workspace-seeding kernel, as inside the step."""
+        if not hasattr(self, "_q8"):
+            self._q8, self._w8 = self.h.quant_q_fp8(self.q, self.w)
+        c = self.case
+        return self.h._C.mqa_logits_hist(self._q8.unsqueeze(1), self.kv, self._w8, self.lens, self.bt, c.width,
+                                         c.group, 0, 1 if c.group == 1 else self.h._MQA_RPC,
+                                         self.lens if hist else None)
+
+    def tokens(self):
+        return self.case.tokens_scored()
+
+    def logits_bytes(self):
+        """Algorithmic HBM bytes of one logits launch: each request's K tokens once (132 B),
+        q8 + w per row, block table entries, logits written for t < len, mask words written."""
+        c = self.case
+        L = c.context_lens.clamp(max=c.width).long()
+        req_tokens = L.view(-1, c.group).max(1).values
+        H = c.q.shape[1]
+        return int(req_tokens.sum() * 132 + c.rows * H * (128 + 4) + ((req_tokens + 63) // 64).sum() * 4
+                   + L.sum() * 4 + c.rows * (c.width // 16) * 2)
+
+    def path_bytes(self):
+        """Algorithmic bytes of the step (the decode byte formula): K once per request, q bf16,
+        w, block table, logits written and read, mask written and read, page-table gather + out."""
+        c = self.case
+        L = c.context_lens.clamp(max=c.width).long()
+        req_tokens = L.view(-1, c.group).max(1).values
+        H = c.q.shape[1]
+        return int(req_tokens.sum() * 132 + c.rows * H * 128 * 2 + c.rows * H * 4 + ((req_tokens + 63) // 64).sum() * 4
+                   + 2 * L.sum() * 4 + 2 * (L.sum() // 16) * 2 + c.rows * 2048 * 8)
+
+
+def decode_cpu_baseline(case, budget_s):
+    """Oracle's torch-CPU indexer on whole query rows, in row order, until budget_s of CPU time."""
+    import numpy as np
+    import torch
+    from oracle import indexer as O
+    from oracle.fp8 import fp8_decode
+    q8, w = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
+    kv = case.kv.view(case.kv.shape[0], -1).numpy()
+    tokens = 0
+    rows = 0
+    lens = case.context_lens.clamp(max=case.width).numpy()
+    t0 = time.perf_counter()
+    for g0 in range(0, case.rows, case.group):
+        # paged K gather + dequant once per request, shared by the request's rows
+        n = int(lens[g0:g0 + case.group].max())
+        slots = O.slots_of(case.block_table.numpy()[g0], n)
+        codes, sc = O.kv_tokens(kv, slots)
+        kf, st, sl = torch.from_numpy(fp8_decode(codes)), torch.from_numpy(sc), torch.from_numpy(slots.astype(np.int32))
+        for r in range(g0, g0 + case.group):
+            L = int(lens[r])
+            O.cpu_indexer_row_torch(torch.from_numpy(fp8_decode(q8[r])), torch.from_numpy(w[r]), kf[:L], st[:L],
+                                    sl[:L])
+            tokens += L
+            rows += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return tokens / 1e3 / dt, f"{rows} of {case.rows} query rows ({tokens} keys scored) in {dt:.1f} s"
+
+
+# ---------------------------------------------------------------------------------------------
+# Prefill
+
+class PrefillStep:
+    SLAB = 4096
+
+    def __init__(self, case, dev):
+        import torch
+        import hcu_ops
+        self.h = hcu_ops
+        self.case = case
+        g = lambda t: t.to(dev)
+        self.q, self.w, self.kv, self.bt, self.lens = g(case.q), g(case.w), g(case.kv), g(case.block_table), \
+            g(case.lens)
+        self.slots = g(case.slots())
+        self.pt = self.slots.view(1, -1)
+        self.width = case.n_keys
+        self.out = torch.empty(case.rows, 2048, dtype=torch.int32, device=dev)
+        self.slab = min(self.SLAB, case.rows)
+        tail = case.rows % self.slab
+        self.cu = torch.tensor([0, self.slab], dtype=torch.int32, device=dev)
+        self.cu_tail = torch.tensor([0, tail if tail else self.slab], dtype=torch.int32, device=dev)
+
+    def __call__(self):
+        h = self.h
+        self.kbf16 = h.dequant_k_paged(self.kv, self.slots)
+        q8, w = h.quant_q_fp8(self.q, self.w)
+        for r0 in range(0, self.case.rows, self.slab):
+            r1 = min(r0 + self.slab, self.case.rows)
+            lg = h.mqa_logits_prefill(q8[r0:r1], w[r0:r1], self.kv, self.bt, self.lens[r0:r1], self.width)
+            cu = self.cu if r1 - r0 == self.slab else self.cu_tail
+            self.out[r0:r1] = h.topk_transform(lg, self.lens[r0:r1], self.pt, cu)
+        return self.out
+
+    def logits_only(self):
+        if not hasattr(self, "_q8"):
+            self._q8, self._w8 = self.h.quant_q_fp8(self.q, self.w)
+        r1 = self.slab
+        return self.h.mqa_logits_prefill(self._q8[:r1], self._w8[:r1], self.kv, self.bt, self.lens[:r1], self.width)
+
+    def tokens(self):
+        return self.case.tokens_scored()
+
+    def logits_flops(self):
+        """fp8 MFMA flops of one logits launch (the first slab): 2 * H * 128 per (row, key)."""
+        H = self.case.q.shape[1]
+        return 2 * H * 128 * int(self.case.lens[:self.slab].long().sum())
+
+    def path_flops(self):
+        H = self.case.q.shape[1]
+        return 2 * H * 128 * self.case.tokens_scored()
+
+
+def prefill_cpu_baseline(case, budget_s):
+    """Oracle's torch-CPU indexer on query rows spread over the causal range (every k-th row)
+    until budget_s; extrapolated per scored key."""
+    import numpy as np
+    import torch
+    from oracle import indexer as O
+    from oracle.fp8 import fp8_decode
+    kv = case.kv.view(case.kv.shape[0], -1).numpy()
+    order = np.concatenate([np.arange(0, case.rows, 97), np.arange(48, case.rows, 97)])
+    tokens = 0
+    rows = 0
+    t0 = time.perf_counter()
+    slots = O.slots_of(case.block_table.numpy(), case.n_keys)  # paged K dequant, once per chunk
+    codes, sc = O.kv_tokens(kv, slots)
+    kf = torch.from_numpy(fp8_decode(codes))
+    st = torch.from_numpy(sc)
+    sl = torch.from_numpy(slots.astype(np.int32))
+    for r in order:
+        q8, w = O.quant_q(case.q[r:r + 1].view(torch.int16).numpy().view(np.uint16), case.w[r:r + 1].numpy())
+        L = int(case.lens[r])
+        O.cpu_indexer_row_torch(torch.from_numpy(fp8_decode(q8[0])), torch.from_numpy(w[0]), kf[:L], st[:L], sl[:L])
+        tokens += L
+        rows += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return tokens / 1e3 / dt, (f"{rows} of {case.rows} query rows spread over the causal range ({tokens} keys "
+                               f"scored) in {dt:.1f} s, extrapolated per scored key")
+
+
+# ---------------------------------------------------------------------------------------------
+
+def graph_of(fn, torch):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def kernel_time_ms(fn, torch, reps=20, rounds=5):
+    """Average duration of fn's launch: a graph of `reps` back-to-back launches, replayed and
+    timed with HIP events on the current stream; median over rounds."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(rounds):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) / reps)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode_mtp64", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs the indexer on one GPU only: this build has no multi-GPU path "
+              "(decode rows shard by request with no exchange between GPUs). Use --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from hcu_ops import workloads as wl
+
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    case = getattr(wl, args.workload)()
+    log(f"built {args.workload} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
+    decode = args.workload.startswith("decode")
+    step = DecodeStep(case, dev) if decode else PrefillStep(case, dev)
+    torch.cuda.synchronize()
+
+    g = graph_of(step, torch)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} graph replays)")
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    tokens = step.tokens()
+    value = tokens / 1e3 / (ms / 1e3)
+    log(f"timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
+
+    k_ms = kernel_time_ms(step.logits_only, torch)
+    if decode:
+        kh_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
+        kb = step.logits_bytes()
+        achieved = kb / (k_ms / 1e3) / 1e9
+        roofline = {"bound": "hbm", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": None, "algorithmic_bytes": kb, "kernel_us": round(k_ms * 1e3, 2),
+                    "with_fused_pass1_us": round(kh_ms * 1e3, 2)}
+        pb = step.path_bytes()
+        pa = pb / (ms / 1e3) / 1e9
+        path = {"bound": "hbm", "achieved": round(pa, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(pa / HBM_PEAK_GBS, 4), "algorithmic_bytes": pb}
+    else:
+        kf = step.logits_flops()
+        achieved = kf / (k_ms / 1e3) / 1e12
+        roofline = {"bound": "mfma", "kernel": "mqa_logits_prefill_kernel", "achieved": round(achieved, 1),
+                    "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                    "traffic": None, "algorithmic_flops": kf, "kernel_us": round(k_ms * 1e3, 2)}
+        pf = step.path_flops()
+        pa = pf / (ms / 1e3) / 1e12
+        path = {"bound": "mfma", "achieved": round(pa, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(pa / FP8_PEAK_TFLOPS, 4), "algorithmic_flops": pf}
+    log(f"logits kernel {k_ms * 1e3:.1f} us -> {roofline['achieved']} {roofline['unit']} ({roofline['frac']:.1%})")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cores = torch.get_num_threads()
+        v, sample = (decode_cpu_baseline if decode else prefill_cpu_baseline)(case, args.cpu_budget)
+        cpu = {"value": round(v, 2), "unit": "K-tokens/s", "cores": cores, "kind": "port",
+               "sample": sample, "cpu": cpu_model()}
+        log(f"cpu baseline {v:.4g} K-tokens/s on {cores} threads ({sample})")
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "K-tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)", "data": "synthetic (seeded, see workloads.py)",
+        "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "query_rows": int(case.rows),
+                   "tokens_scored_per_step": int(tokens), "graph": "hipGraph replay per step"},
+        "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

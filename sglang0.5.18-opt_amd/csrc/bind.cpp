@@ -4,7 +4,8 @@
 // a drop-in; outputs and workspaces come from the caching allocator on the input's device and
 // all work goes to the current HIP stream, so every call can be captured in a hipGraph.
 #include <ATen/hip/HIPContext.h>
-#include <c10/hip/HIPGuard.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/extension.h>
 
 #include <algorithm>
@@ -20,7 +21,8 @@ constexpr int64_t kHeadDim = DSA_HEAD_DIM;
 constexpr int64_t kTopK = DSA_TOPK;
 constexpr int64_t kBins = 4096;
 
-hipStream_t cur_stream() { return c10::hip::getCurrentHIPStream().stream(); }
+// PyTorch-ROCm tensors report device type "cuda": use the guard / stream that masquerade as it.
+hipStream_t cur_stream() { return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
 
 void check_status(int st) { TORCH_CHECK(st == DSA_OK, dsa_last_error()); }
 
@@ -69,7 +71,7 @@ std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::
                     hist_lens->is_contiguous(),
                 "hist_lens must be contiguous int32 [B]");
   }
-  const c10::hip::HIPGuard guard(q.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto logits = torch::empty({B, max_context_len}, q.options().dtype(at::kFloat));
   const int64_t mask_stride = (max_context_len + 15) / 16;
   auto mask = torch::empty({B, mask_stride}, q.options().dtype(at::kShort));
@@ -122,7 +124,7 @@ torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::T
                     cu_seqlens_q.size(0) == page_table_size_1.size(0) + 1,
                 "varlen layout needs int32 cu_seqlens_q [requests + 1] with one page-table row per request");
   }
-  const c10::hip::HIPGuard guard(score.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(score.device());
   auto dst = torch::empty({rows, kTopK}, score.options().dtype(at::kInt));
   if (rows == 0) return dst;
   const int cus = n_cu();
@@ -185,7 +187,7 @@ torch::Tensor dequant_k_paged(const torch::Tensor& kv_cache, const torch::Tensor
   check_kv(kv_cache);
   TORCH_CHECK(slots.scalar_type() == at::kInt && slots.dim() == 1 && slots.is_contiguous(),
               "slots must be contiguous int32 [n]");
-  const c10::hip::HIPGuard guard(kv_cache.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(kv_cache.device());
   const int64_t n = slots.size(0);
   auto out = torch::empty({n, kHeadDim}, kv_cache.options().dtype(at::kBFloat16));
   check_status(dsa_dequant_k_paged(kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), slots.data_ptr<int>(), n,
@@ -197,7 +199,7 @@ std::vector<torch::Tensor> gather_k_paged(const torch::Tensor& kv_cache, const t
   check_kv(kv_cache);
   TORCH_CHECK(slots.scalar_type() == at::kInt && slots.dim() == 1 && slots.is_contiguous(),
               "slots must be contiguous int32 [n]");
-  const c10::hip::HIPGuard guard(kv_cache.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(kv_cache.device());
   const int64_t n = slots.size(0);
   auto k8 = torch::empty({n, kHeadDim}, kv_cache.options().dtype(at::kFloat8_e4m3fn));
   auto sc = torch::empty({n}, kv_cache.options().dtype(at::kFloat));
@@ -217,7 +219,7 @@ torch::Tensor dequantize_k_cache_paged(const torch::Tensor& quant_k_cache, const
   TORCH_CHECK(page_table_1_flattened.scalar_type() == at::kInt && page_table_1_flattened.dim() == 1 &&
                   page_table_1_flattened.is_contiguous(),
               "page_table_1_flattened must be contiguous int32 [n]");
-  const c10::hip::HIPGuard guard(quant_k_cache.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(quant_k_cache.device());
   const int64_t n = page_table_1_flattened.size(0);
   auto out = torch::empty({n, 1, 576}, quant_k_cache.options().dtype(at::kBFloat16));
   check_status(dsa_dequant_mla_paged(reinterpret_cast<const uint8_t*>(qk.data_ptr()), qk.stride(0),
@@ -234,7 +236,7 @@ std::vector<torch::Tensor> quant_q_fp8(const torch::Tensor& q, const torch::Tens
   const int64_t rows = q.numel() / (H * kHeadDim);
   TORCH_CHECK(weights.scalar_type() == at::kFloat && weights.is_contiguous() && weights.numel() == rows * H,
               "weights must be contiguous float32 with rows * H elements");
-  const c10::hip::HIPGuard guard(q.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto q8 = torch::empty(q.sizes(), q.options().dtype(at::kFloat8_e4m3fn));
   auto w_eff = torch::empty(weights.sizes(), weights.options());
   check_status(dsa_quant_q_fp8(reinterpret_cast<const uint16_t*>(q.data_ptr()), weights.data_ptr<float>(), rows,
@@ -251,7 +253,7 @@ void store_k_cache(const torch::Tensor& k, const torch::Tensor& slots, torch::Te
   TORCH_CHECK(slots.scalar_type() == at::kInt && slots.dim() == 1 && slots.size(0) == k.size(0) &&
                   slots.is_contiguous(),
               "slots must be contiguous int32 [n]");
-  const c10::hip::HIPGuard guard(k.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
   check_status(dsa_store_k_cache(reinterpret_cast<const uint16_t*>(k.data_ptr()), k.size(0), slots.data_ptr<int>(),
                                  kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), cur_stream()));
 }
@@ -273,7 +275,7 @@ torch::Tensor mqa_logits_prefill(const torch::Tensor& q, const torch::Tensor& we
   TORCH_CHECK(lens.scalar_type() == at::kInt && lens.dim() == 1 && lens.size(0) == rows && lens.is_contiguous(),
               "lens must be contiguous int32 [rows]");
   TORCH_CHECK(width > 0 && width <= block_table.size(0) * kPage, "width must be within the block table capacity");
-  const c10::hip::HIPGuard guard(q.device());
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto logits = torch::empty({rows, width}, q.options().dtype(at::kFloat));
   check_status(dsa_mqa_logits_prefill(reinterpret_cast<const uint8_t*>(q.data_ptr()), weights.data_ptr<float>(),
                                       static_cast<int>(H), rows, kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0),

@@ -253,18 +253,16 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 
 // Seeds the top-k pass-1 workspace: every token below min(hist_len, width) counts as a zero
 // until the logits kernel subtracts its nonzero ones.  Rows with <= 2048 tokens stay empty.
+// The second histogram block of the layout ([ghist1 | ghist2 | cnt], kept for the reference's
+// workspace size) is not used by this top-k and is left unwritten.
 __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __restrict__ hist_lens, int width,
                                                             int64_t batch, int32_t* __restrict__ ws) {
   const int64_t row = blockIdx.x;
   int h = hist_lens[row];
   h = h < width ? h : width;
   const int zeros = h > kTopK ? h : 0;
-  int32_t* g1 = ws + row * kBins;
-  int32_t* g2 = ws + (batch + row) * kBins;
-  for (int i = threadIdx.x; i < kBins; i += 256) {
-    g1[i] = i == kZeroBin ? zeros : 0;
-    g2[i] = 0;
-  }
+  int4* g1 = reinterpret_cast<int4*>(ws + row * kBins);
+  for (int i = threadIdx.x; i < kBins / 4; i += 256) g1[i] = make_int4(i == kZeroBin / 4 ? zeros : 0, 0, 0, 0);
   if (threadIdx.x == 0) {
     int32_t* c = ws + 2 * batch * kBins + 2 * row;
     c[0] = 0;

@@ -5,12 +5,15 @@ import torch
 from oracle import indexer as O
 from oracle.fp8 import fp8_decode
 
-# Logits tolerance: |gpu - oracle| <= RTOL * A_t, where A_t = s_t * sum_h |w_h| relu(acc_h) is the
-# magnitude of the weighted ReLU sum (A_t = |logit| when the head weights share a sign, A_t >=
-# |logit| otherwise); in addition at least STRICT_FRAC of the tokens must meet the plain
-# relative bound |gpu - oracle| <= RTOL * |oracle|.
+# Logits tolerance (fp32 accumulation on fp8 MFMA vs the exact fp64 oracle):
+#  (a) every token: |gpu - oracle| <= RTOL * A_t, where A_t = s_t * sum_h |w_h| relu(acc_h) is the
+#      magnitude of the weighted ReLU sum (A_t = |logit| when the head weights share a sign);
+#  (b) tokens whose logit is not cancelled by more than CANCEL across heads (|logit| >= A_t /
+#      CANCEL): the plain relative bound |gpu - oracle| <= RTOL * |oracle|.
+# Near-total cancellation (|logit| << A_t) amplifies any fp32 rounding, an fp32 reference's own
+# included, so (b) excludes it and (a) bounds it.
 RTOL = 1e-3
-STRICT_FRAC = 0.999
+CANCEL = 20.0
 
 
 def kv_np(kv):
@@ -22,13 +25,17 @@ def q_bits(q_bf16):
 
 
 def check_logits(got, ref, mag, what=""):
+    """Asserts the tolerance above; returns (max err / A_t, max relative err over (b))."""
     got = np.asarray(got, dtype=np.float64)
     err = np.abs(got - ref)
     bad = err > RTOL * mag + 1e-30
-    assert not bad.any(), f"{what}: {int(bad.sum())} logits outside {RTOL} * magnitude; worst " \
-                          f"{float((err / np.maximum(mag, 1e-30)).max()):.3e}"
-    strict = (err <= RTOL * np.abs(ref)).mean() if ref.size else 1.0
-    assert strict >= STRICT_FRAC, f"{what}: only {strict:.5f} of logits within {RTOL} relative"
+    worst_mag = float((err / np.maximum(mag, 1e-30)).max()) if err.size else 0.0
+    assert not bad.any(), f"{what}: {int(bad.sum())} logits outside {RTOL} * magnitude; worst {worst_mag:.3e}"
+    plain = np.abs(ref) >= mag / CANCEL
+    rel = err[plain] / np.abs(ref[plain]) if plain.any() else np.zeros(1)
+    worst_rel = float(rel.max())
+    assert worst_rel <= RTOL, f"{what}: relative error {worst_rel:.3e} > {RTOL} on an uncancelled logit"
+    return worst_mag, worst_rel
 
 
 def sorted_rows(a):
@@ -44,5 +51,5 @@ def oracle_q(case):
     return O.quant_q(q_bits(case.q), case.w.numpy())
 
 
-__all__ = ["RTOL", "STRICT_FRAC", "kv_np", "q_bits", "check_logits", "sorted_rows", "oracle_decode", "oracle_q",
+__all__ = ["RTOL", "CANCEL", "kv_np", "q_bits", "check_logits", "sorted_rows", "oracle_decode", "oracle_q",
            "fp8_decode"]
