@@ -98,16 +98,19 @@ int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* s
  * logits [B, width] f32 with row stride logits_stride; entries t >= len[r] are not written.
  * mask [B, width / 16] i16 with row stride mask_stride: every word is written.
  * heads in {32, 64}; B % group_size == 0; rows_per_cta divides group_size and is in {1,2,3,4}.
- * pages_per_cta <= 0 picks the default.
+ * target_ctas: number of CTAs the K pages are spread over, each CTA streaming a slice of one
+ * request (<= 0: twice the CU count); the grid is target_ctas + B / rows_per_cta.
  * hist_lens (nullable, int32 [B]) with hist_ws (int32 [B * (2 * 4096 + 2)]): also build pass 1
  * of the top-k (12-bit key histogram + positive / zero counts of every row whose
- * min(hist_lens[r], width) > 2048) into hist_ws, in the layout dsa_topk_transform_pre consumes. */
+ * min(hist_lens[r], width) > 2048) into hist_ws, in the layout dsa_topk_transform_pre consumes:
+ * [12-bit histograms rows*4096 | second block rows*4096 | (positives, zeros) rows*2]; of the
+ * second block only word 0 of each row is written (zero, the top-k's output counter). */
 int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t batch,
                           int group_size, const uint8_t* kv_cache, int64_t page_stride_bytes,
                           const int32_t* context_lens, const int32_t* block_table,
                           int64_t bt_stride, int64_t bt_pages, float* logits,
                           int64_t logits_stride, int16_t* mask, int64_t mask_stride,
-                          int rows_per_cta, int pages_per_cta, const int32_t* hist_lens,
+                          int rows_per_cta, int target_ctas, const int32_t* hist_lens,
                           int32_t* hist_ws, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
@@ -153,12 +156,13 @@ int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
 /* dsa_topk_transform with pass 1 (histogram and counts) already built into hist_ws by
  * dsa_mqa_logits_decode(hist_lens = lengths) (replaces
  * _C.sparse_mask_topk_transform_split_pre, sparse_mask_topk.cu:986-1051).  hist_ws is the
- * int32 [rows * (2 * 4096 + 2)] buffer given to the logits call; `workspace` as above. */
+ * int32 [rows * (2 * 4096 + 2)] buffer given to the logits call (its per-row output counter is
+ * updated, so a hist_ws serves one top-k call); `workspace` as above. */
 int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t width,
                            const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
                            int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
                            const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
-                           const int32_t* hist_ws, void* workspace, size_t workspace_bytes,
+                           int32_t* hist_ws, void* workspace, size_t workspace_bytes,
                            int32_t* out, hipStream_t stream);
 
 #ifdef __cplusplus

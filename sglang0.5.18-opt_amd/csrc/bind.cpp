@@ -40,8 +40,8 @@ void check_kv(const torch::Tensor& kv_cache) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Logits (hcu_ops/csrc/mqa_hist.cu:324-405).  persistent_ctas keeps its meaning of "CTAs per
-// request" (<= 0: default split of 8 pages per CTA); hist_lens builds top-k pass 1 into zws.
+// Logits (hcu_ops/csrc/mqa_hist.cu:324-405).  persistent_ctas > 0 sets the number of CTAs the
+// K pages are spread over (<= 0: twice the CU count); hist_lens builds top-k pass 1 into zws.
 std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::Tensor& kv_cache,
                                            const torch::Tensor& weights, const torch::Tensor& context_lens,
                                            const torch::Tensor& block_table, int64_t max_context_len,
@@ -77,12 +77,12 @@ std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::
   auto mask = torch::empty({B, mask_stride}, q.options().dtype(at::kShort));
   auto zws = torch::empty({hist ? B * (2 * kBins + 2) : 0}, q.options().dtype(at::kInt));
   const int64_t pages = block_table.size(1);
-  const int64_t ppc = persistent_ctas > 0 ? (pages + persistent_ctas - 1) / persistent_ctas : 0;
+  const int target = static_cast<int>(std::min<int64_t>(std::max<int64_t>(persistent_ctas, 0), 1 << 20));
   check_status(dsa_mqa_logits_decode(
       reinterpret_cast<const uint8_t*>(q.data_ptr()), weights.data_ptr<float>(), static_cast<int>(H), B,
       static_cast<int>(group_size), kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), context_lens.data_ptr<int>(),
       block_table.data_ptr<int>(), block_table.stride(0), pages, logits.data_ptr<float>(), logits.stride(0),
-      mask.data_ptr<int16_t>(), mask_stride, static_cast<int>(rows_per_cta), static_cast<int>(ppc),
+      mask.data_ptr<int16_t>(), mask_stride, static_cast<int>(rows_per_cta), target,
       hist ? hist_lens->data_ptr<int>() : nullptr, hist ? zws.data_ptr<int>() : nullptr, cur_stream()));
   return {logits, mask, zws};
 }

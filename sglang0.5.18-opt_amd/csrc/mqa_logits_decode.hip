@@ -15,14 +15,19 @@
 //  * Result lane l holds heads 4*(l/16)+i of token l%16: the epilogue is an in-lane
 //    max/fma chain over H/4 values, two xor-shuffles (16, 32), and a lane select that leaves
 //    lane l with token l of the page.  One 256 B logits store and one K-scale load per page.
-//  * Each CTA (4 waves) owns `ppc` consecutive pages of one row group (R rows of a request);
-//    wave w takes pages w, w+4, ... and prefetches its next page while computing the current.
-//    Grid = chunks x row groups, row groups fastest.  CTAs whose pages lie past the rows'
-//    lengths only zero their mask words, so no separate mask memset is launched.
+//  * Balanced static grid: a row group is R rows of one request (one K page stream feeds all R
+//    rows).  Every CTA reads the groups' lengths and gives group g ceil(pages_g * T / P) CTAs
+//    (P = total pages, T = the target CTA count), so each CTA streams ~P / T consecutive pages of
+//    a single group whatever the length mix; the grid (T + groups) depends only on shapes, so
+//    the launch can be captured in a hipGraph.  The CTA's block-table slice is staged in LDS; its
+//    4 waves take pages w, w+4, ... and prefetch the next page while computing the current one.
+//  * Mask words of pages past a group's length are zeroed by CTA g (grid >= groups), so no
+//    separate mask memset is launched.
 //  * kHist: also the top-k pass-1 histogram (12-bit key[31:20] of the nonzero logits of rows
-//    with min(hist_len, width) > 2048, plus positive / zero counts), as LDS counts flushed with
-//    one global atomic per nonzero bin; mqa_hist_init_kernel seeds the zero bin / zero count
-//    with the row length (mqa_hist.cu:278-304) and every CTA subtracts its nonzero tokens.
+//    with min(hist_len, width) > 2048, plus positive / zero counts), as LDS counts flushed once
+//    per CTA with one global atomic per nonzero bin; mqa_hist_init_kernel seeds the zero bin /
+//    zero count with the row length (mqa_hist.cu:278-304) and every CTA subtracts its nonzero
+//    tokens.
 #include "dsa_common.h"
 
 namespace dsa {
@@ -34,6 +39,7 @@ using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerCta = kThreads / kWave;
+constexpr int kMaxCtaPages = 1024;  // host keeps P / T <= 1024 so the block-table slice fits LDS
 
 __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
   // scale operands 0 select the unscaled v_mfma_f32_16x16x128_f8f6f4 (both operands fp8 e4m3)
@@ -82,35 +88,115 @@ struct DecodeArgs {
   int16_t* mask;
   int64_t mask_stride;
   int group;
-  int n_rowgroups;  // batch / R
-  int ppc;          // pages per CTA
+  int R;
+  int n_groups;  // batch / R
+  int target;    // T: CTAs the pages are spread over
   const int32_t* hist_lens;
   int32_t* hist_ws;
   int64_t batch;
 };
+
+__device__ __forceinline__ int clamp_len(int l, int width) { return l < 0 ? 0 : (l > width ? width : l); }
+
+// Pages of row group g: ceil(max over its R rows of len / 64).
+__device__ __forceinline__ int group_pages(const DecodeArgs& a, int g) {
+  int m = 0;
+  for (int r = 0; r < a.R; ++r) m = max(m, clamp_len(a.ctx[g * a.R + r], a.width));
+  return (m + kPage - 1) / kPage;
+}
+
+__device__ __forceinline__ int group_ctas(int pages, int total_pages, int target) {
+  if (pages == 0) return 0;
+  return static_cast<int>((static_cast<int64_t>(pages) * target + total_pages - 1) / total_pages);
+}
+
+// Block-wide (256 threads) sum and exclusive prefix.
+__device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  int inc = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) s_w[w] = inc;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int v = 0; v < kWavesPerCta; ++v) {
+    before += v < w ? s_w[v] : 0;
+    tot += s_w[v];
+  }
+  __syncthreads();
+  total = tot;
+  return before + inc - x;
+}
 
 template <int H, int R, bool kHist>
 __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const DecodeArgs a) {
   constexpr int HT = H / 16;  // head tiles
   extern __shared__ int s_hist[];  // kHist: [R][kBins]
   __shared__ int s_cnt[2 * R];
+  __shared__ int s_w[kWavesPerCta];
+  __shared__ int s_assign[3];  // group, index within the group's CTAs, the group's CTA count
+  __shared__ int s_bt[kMaxCtaPages];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int rg = static_cast<int>(blockIdx.x % static_cast<uint32_t>(a.n_rowgroups));
-  const int chunk = static_cast<int>(blockIdx.x / static_cast<uint32_t>(a.n_rowgroups));
-  const int row0 = rg * R;
-  const int group_row = (row0 / a.group) * a.group;
+  const int cta = blockIdx.x;
 
+  // ---- work assignment (identical in every CTA) ----
+  const int per_t = (a.n_groups + kThreads - 1) / kThreads;
+  const int g_lo = min(tid * per_t, a.n_groups);
+  const int g_hi = min(g_lo + per_t, a.n_groups);
+  int my_pages = 0;
+  for (int g = g_lo; g < g_hi; ++g) my_pages += group_pages(a, g);
+  int total_pages;
+  block_excl(my_pages, total_pages, s_w);
+  if (tid == 0) s_assign[0] = -1;
+  int my_ctas = 0;
+  for (int g = g_lo; g < g_hi; ++g) my_ctas += group_ctas(group_pages(a, g), total_pages, a.target);
+  int total_ctas;
+  int c0 = block_excl(my_ctas, total_ctas, s_w);
+  if (cta >= c0 && cta < c0 + my_ctas) {
+    for (int g = g_lo; g < g_hi; ++g) {
+      const int n = group_ctas(group_pages(a, g), total_pages, a.target);
+      if (cta < c0 + n) {
+        s_assign[0] = g;
+        s_assign[1] = cta - c0;
+        s_assign[2] = n;
+        break;
+      }
+      c0 += n;
+    }
+  }
+
+  // ---- mask words past group `cta`'s pages (grid >= groups, so every group has an owner) ----
+  if (cta < a.n_groups) {
+    const int p0 = group_pages(a, cta);
+    const int words = (a.bt_pages - p0) * 4;
+    for (int r = 0; r < R; ++r) {
+      int16_t* m = a.mask + static_cast<int64_t>(cta * R + r) * a.mask_stride + p0 * 4;
+      for (int i = tid; i < words; i += kThreads) m[i] = 0;
+    }
+  }
+  __syncthreads();
+  const int grp = s_assign[0];
+  if (grp < 0) return;  // uniform: no pages for this CTA
+  const int j = s_assign[1];
+  const int nj = s_assign[2];
+
+  const int row0 = grp * R;
+  const int group_row = (row0 / a.group) * a.group;
   int len[R];
   int hlim[R];
   int max_len = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int l = a.ctx[row0 + r];
-    len[r] = l < 0 ? 0 : (l > a.width ? a.width : l);
-    max_len = len[r] > max_len ? len[r] : max_len;
+    len[r] = clamp_len(a.ctx[row0 + r], a.width);
+    max_len = max(max_len, len[r]);
     hlim[r] = 0;
     if constexpr (kHist) {
       int h = a.hist_lens[row0 + r];
@@ -118,26 +204,18 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
       hlim[r] = h > kTopK ? h : 0;
     }
   }
-  const int n_pages = (max_len + kPage - 1) / kPage;
-  const int p_begin = chunk * a.ppc;
-  const int p_end = min(p_begin + a.ppc, a.bt_pages);
-  const int p_live = min(p_end, n_pages);
+  const int pages = (max_len + kPage - 1) / kPage;
+  const int p_begin = static_cast<int>(static_cast<int64_t>(pages) * j / nj);
+  const int p_end = static_cast<int>(static_cast<int64_t>(pages) * (j + 1) / nj);
+  const int n_local = p_end - p_begin;  // <= kMaxCtaPages by the host's choice of target
 
-  // Mask words of pages past every row's length: zero them (4 words per page and row).
-  for (int p0 = max(p_begin, n_pages); p0 < p_end; p0 += kThreads / 4) {
-    const int p = p0 + (tid >> 2);
-    if (p < p_end) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) a.mask[static_cast<int64_t>(row0 + r) * a.mask_stride + p * 4 + (tid & 3)] = 0;
-    }
-  }
-  if (p_begin >= p_live) return;  // uniform over the CTA, before any barrier
-
+  const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride + p_begin;
+  for (int i = tid; i < n_local; i += kThreads) s_bt[i] = btr[i];
   if constexpr (kHist) {
     for (int i = tid; i < R * kBins; i += kThreads) s_hist[i] = 0;
     if (tid < 2 * R) s_cnt[tid] = 0;
-    __syncthreads();
   }
+  __syncthreads();
 
   // q / w fragments (see header comment for the lane mapping).
   i32x8 qf[R][HT];
@@ -155,20 +233,19 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
     }
   }
 
-  const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride;
   int nz[R], pos[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) nz[r] = pos[r] = 0;
 
-  int p = p_begin + wave;
-  if (p < p_live) {
+  int i = wave;
+  if (i < n_local) {
     PageRegs cur;
-    load_page(a.kv, a.page_stride, uniform(btr[p]), lane, cur);
+    load_page(a.kv, a.page_stride, s_bt[i], lane, cur);
     while (true) {
-      const int pn = p + kWavesPerCta;
+      const int in = i + kWavesPerCta;
       PageRegs nxt;
       // Branch-free prefetch: past the end the current page is loaded again.
-      load_page(a.kv, a.page_stride, uniform(btr[pn < p_live ? pn : p]), lane, nxt);
+      load_page(a.kv, a.page_stride, s_bt[in < n_local ? in : i], lane, nxt);
 
       float val[R];
 #pragma unroll
@@ -184,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s += fmaxf(acc[ht][i], 0.0f) * wf[r][ht * 4 + i];
+            for (int e = 0; e < 4; ++e) s += fmaxf(acc[ht][e], 0.0f) * wf[r][ht * 4 + e];
           }
           s += __shfl_xor(s, 16);
           s += __shfl_xor(s, 32);
@@ -192,6 +269,7 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
         }
       }
 
+      const int p = p_begin + i;
       const int token = p * kPage + lane;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -212,8 +290,8 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
         }
       }
 
-      p = pn;
-      if (p >= p_live) break;
+      i = in;
+      if (i >= n_local) break;
       cur = nxt;
     }
   }
@@ -234,9 +312,9 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
       if (hlim[r] == 0) continue;
       int32_t* gh = a.hist_ws + static_cast<int64_t>(row0 + r) * kBins;
       int32_t* gcnt = a.hist_ws + 2 * a.batch * kBins + 2 * static_cast<int64_t>(row0 + r);
-      for (int i = tid; i < kBins; i += kThreads) {
-        const int c = s_hist[r * kBins + i];
-        if (c) atomicAdd(&gh[i], c);
+      for (int b = tid; b < kBins; b += kThreads) {
+        const int c = s_hist[r * kBins + b];
+        if (c) atomicAdd(&gh[b], c);
       }
       if (tid == 0) {
         const int n = s_cnt[2 * r];
@@ -253,8 +331,8 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 
 // Seeds the top-k pass-1 workspace: every token below min(hist_len, width) counts as a zero
 // until the logits kernel subtracts its nonzero ones.  Rows with <= 2048 tokens stay empty.
-// The second histogram block of the layout ([ghist1 | ghist2 | cnt], kept for the reference's
-// workspace size) is not used by this top-k and is left unwritten.
+// Of the second histogram block of the layout ([ghist1 | ghist2 | cnt], the reference's
+// workspace size) only word 0 of each row is used -- as the top-k's output counter -- and zeroed.
 __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __restrict__ hist_lens, int width,
                                                             int64_t batch, int32_t* __restrict__ ws) {
   const int64_t row = blockIdx.x;
@@ -267,6 +345,7 @@ __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __res
     int32_t* c = ws + 2 * batch * kBins + 2 * row;
     c[0] = 0;
     c[1] = zeros;
+    ws[(batch + row) * kBins] = 0;
   }
 }
 
@@ -297,7 +376,7 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
                                      const uint8_t* kv_cache, int64_t page_stride_bytes,
                                      const int32_t* context_lens, const int32_t* block_table, int64_t bt_stride,
                                      int64_t bt_pages, float* logits, int64_t logits_stride, int16_t* mask,
-                                     int64_t mask_stride, int rows_per_cta, int pages_per_cta,
+                                     int64_t mask_stride, int rows_per_cta, int target_ctas,
                                      const int32_t* hist_lens, int32_t* hist_ws, hipStream_t stream) {
   DSA_REQUIRE(heads == 32 || heads == 64, "dsa_mqa_logits_decode: heads must be 32 or 64 (got %d)", heads);
   DSA_REQUIRE(batch >= 0 && group_size >= 1, "dsa_mqa_logits_decode: batch must be >= 0 and group_size >= 1");
@@ -319,11 +398,23 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
               "dsa_mqa_logits_decode: strides smaller than the block table capacity");
   DSA_REQUIRE((hist_lens == nullptr) == (hist_ws == nullptr),
               "dsa_mqa_logits_decode: hist_lens and hist_ws go together");
-  if (pages_per_cta <= 0) pages_per_cta = 8;
-  DSA_REQUIRE(pages_per_cta <= 4096, "dsa_mqa_logits_decode: pages_per_cta too large");
   const bool hist = hist_ws != nullptr;  // 32-bit LDS counters: no limit on tokens per CTA
   DSA_REQUIRE(!hist || rows_per_cta <= 3,
               "dsa_mqa_logits_decode: the fused histogram needs rows_per_cta <= 3 (16 KB of LDS per row)");
+  const int64_t n_groups = batch / rows_per_cta;
+  DSA_REQUIRE(n_groups <= 0x3FFFFFFF, "dsa_mqa_logits_decode: batch too large");
+  if (target_ctas <= 0) {
+    int n_cu = 0;
+    const int st = dsa_device_cu_count(&n_cu);
+    if (st != DSA_OK) return st;
+    target_ctas = 2 * n_cu;
+  }
+  // Keep every CTA's page slice within the LDS block-table stage: P / T <= kMaxCtaPages.
+  const int64_t max_pages = n_groups * bt_pages;
+  int64_t target = target_ctas;
+  if (target * kMaxCtaPages < max_pages) target = (max_pages + kMaxCtaPages - 1) / kMaxCtaPages;
+  const int64_t grid = target + n_groups;
+  DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_mqa_logits_decode: grid too large");
 
   DecodeArgs a;
   a.q8 = q8;
@@ -340,14 +431,12 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   a.mask = mask;
   a.mask_stride = mask_stride;
   a.group = group_size;
-  a.n_rowgroups = static_cast<int>(batch / rows_per_cta);
-  a.ppc = pages_per_cta;
+  a.R = rows_per_cta;
+  a.n_groups = static_cast<int>(n_groups);
+  a.target = static_cast<int>(target);
   a.hist_lens = hist_lens;
   a.hist_ws = hist_ws;
   a.batch = batch;
-  const int64_t chunks = (bt_pages + pages_per_cta - 1) / pages_per_cta;
-  const int64_t grid = chunks * a.n_rowgroups;
-  DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_mqa_logits_decode: grid too large");
 
   if (hist) {
     hipLaunchKernelGGL(mqa_hist_init_kernel, dim3(static_cast<uint32_t>(batch)), dim3(256), 0, stream, hist_lens,

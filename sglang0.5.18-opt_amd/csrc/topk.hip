@@ -2,35 +2,38 @@
 //
 // Contract (hcu_ops/csrc/sparse_mask_topk.cu:1-22,141-349): per row, the 2048 tokens t < len
 // with the largest keys, ties at the threshold to the lower t; masked-out tokens are +0;
-// rows with len <= 2048 copy page_table[0:len] and pad with -1.  Only the set is the contract.
+// rows with len <= 2048 copy page_table[0:len] and pad with -1.  Only the set is the contract
+// (the order within a row is unspecified here, as it differs between the reference's variants).
 //
 // Algorithm (this file's own; radix digits 12/12/8 of the 32-bit key):
-//   pass 1   LDS histogram of key[31:20] over the nonzero tokens, positive / zero counts.
-//            positives <= 2048 <= positives + zeros: the threshold is +0 (sparse fast path).
-//   pass 2   one ordered compaction over the row: tokens whose digit is above the threshold
-//            bin t1 go straight to the output (list A); tokens in bin t1 go to an LDS candidate
-//            list C (key, token) in token order.
-//   resolve  key[19:8] and key[7:0] histograms over C in LDS give the exact threshold key and
-//            the number of threshold ties to take; C is emitted in token order, so the ties that
-//            win are the lowest-index ones.
-//   overflow if C does not fit in LDS the two digit passes and the emission re-read the row.
-// So a row is read twice (once if pass 1 comes from the logits kernel) instead of four times.
-// Split variant (few rows): S CTAs per row share pass 1 through global atomics, compact their
-// slice into per-slice global lists, and one CTA per row merges the lists (slices are
-// contiguous token ranges, so slice order is token order) and resolves C.
-// Every loop bound is block-uniform; no host synchronisation; launch shapes depend only on
-// (rows, width, splits), so the whole path can be captured in a hipGraph.
+//   pass 1   histogram of key[31:20] over the nonzero tokens plus positive / zero counts (or
+//            taken from the logits kernel).  positives <= 2048 <= positives + zeros means the
+//            threshold is +0 (sparse fast path).  Otherwise the threshold digit t1 follows.
+//   collect  one unordered pass over the row: tokens above bin t1 (or positive, fast path) are
+//            written straight to the output, tokens in bin t1 become candidates (key, token);
+//            positions come from wave-aggregated LDS atomics, so the streaming loop has no
+//            barriers and keeps several loads in flight per lane.
+//   resolve  the candidates (in LDS) go through the three digit passes to the exact threshold
+//            key and the number `remaining` of threshold ties to take.  If there are more ties
+//            than that, a second radix select over ~token among the ties keeps the lowest
+//            indices.  Fast path: the first `remaining` zeros come from an ordered scan of the
+//            row's prefix, which stops as soon as enough were found.
+//   overflow candidates that do not fit in LDS are resolved by re-reading the row.
+// Few rows: S CTAs per row run pass 1 (global histogram) and the collection of one slice each;
+// one CTA per row then merges the slices' candidates and resolves.  Many rows: one CTA per row
+// does everything.  No host synchronisation; launch shapes depend only on (rows, width,
+// splits), so the whole path can be captured in a hipGraph.
 #include "dsa_common.h"
 
 namespace dsa {
 namespace {
 
-constexpr int kTk = 1024;              // threads per CTA
-constexpr int kTkWaves = kTk / kWave;  // 16
-constexpr int kStep = kTk * 4;         // tokens per block step (4 per thread)
-constexpr int kCapC = 8192;            // LDS candidate capacity (single / merge kernels)
-constexpr int kCapSlice = 4096;        // per-slice candidate capacity in the split workspace
+constexpr int kTk = 1024;       // threads of the single / finish CTAs
+constexpr int kTs = 256;        // threads of the split pass-1 / collect CTAs
+constexpr int kCapC = 8192;     // candidates a row can resolve in LDS
+constexpr int kCapSlice = 4096; // candidates one collect CTA stages (and stores per slice)
 constexpr int kMaxSplit = 64;
+constexpr int kUnroll = 4;      // float4 groups in flight per lane
 
 struct RowSrc {
   const float* vals;
@@ -38,7 +41,8 @@ struct RowSrc {
   int len;
 };
 
-// Keys of tokens [i0, i0 + 4) (i0 % 4 == 0) and the bitmask of those below r.len.
+// Keys of tokens [i0, i0 + 4) (i0 % 4 == 0) and the bitmask of those below r.len.  Past the
+// end the loads are redirected to token 0, so they stay inside the row.
 template <bool kVec>
 __device__ __forceinline__ uint32_t load_keys4(const RowSrc& r, int i0, uint32_t (&k)[4]) {
   const int safe = i0 < r.len ? i0 : 0;
@@ -65,52 +69,54 @@ __device__ __forceinline__ uint32_t load_keys4(const RowSrc& r, int i0, uint32_t
   return (1u << nv) - 1u;
 }
 
-// Block-exclusive prefix of two per-thread counts (each in [0, 4]) in thread order.
-// s_scan: int2[2][kTkWaves], double-buffered by `parity`, so one barrier per call suffices.
-__device__ __forceinline__ void block_prefix2(int ca, int cb, int& pa, int& pb, int& ta, int& tb, int2* s_scan,
-                                              int parity) {
-  int wa, wb;
-  const int xa = wave_prefix_small(ca, wa);
-  const int xb = wave_prefix_small(cb, wb);
-  const int w = threadIdx.x >> 6;
-  int2* buf = s_scan + parity * kTkWaves;
-  if (lane_id() == 0) buf[w] = make_int2(wa, wb);
-  __syncthreads();
-  int ba = 0, bb = 0, sa = 0, sb = 0;
-#pragma unroll
-  for (int v = 0; v < kTkWaves; ++v) {
-    const int2 t = buf[v];
-    ba += v < w ? t.x : 0;
-    bb += v < w ? t.y : 0;
-    sa += t.x;
-    sb += t.y;
-  }
-  pa = ba + xa;
-  pb = bb + xb;
-  ta = sa;
-  tb = sb;
-}
-
+template <int NT>
 __device__ __forceinline__ int block_sum(int x, int* s_red) {
+  constexpr int W = NT / kWave;
   x = wave_sum(x);
   if (lane_id() == 0) s_red[threadIdx.x >> 6] = x;
   __syncthreads();
   int s = 0;
 #pragma unroll
-  for (int v = 0; v < kTkWaves; ++v) s += s_red[v];
+  for (int v = 0; v < W; ++v) s += s_red[v];
   __syncthreads();
   return s;
 }
 
-// Finds bin t with suffix(t) >= need > suffix(t + 1); s_res = {t, suffix(t + 1)}.
-// Requires sum(hist) >= need >= 1.  Ends with a barrier.
-template <int NB>
+// Block-exclusive prefix (thread order) of a per-thread count in [0, 7]; one barrier, with the
+// wave totals double-buffered by `parity` so back-to-back calls do not race.
+template <int NT>
+__device__ __forceinline__ int block_prefix(int c, int& total, int* s_scan, int parity) {
+  constexpr int W = NT / kWave;
+  int wt;
+  const int x = wave_prefix_small(c, wt);
+  const int w = threadIdx.x >> 6;
+  int* buf = s_scan + parity * W;
+  if (lane_id() == 0) buf[w] = wt;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int v = 0; v < W; ++v) {
+    before += v < w ? buf[v] : 0;
+    tot += buf[v];
+  }
+  total = tot;
+  return before + x;
+}
+
+// Finds bin t with suffix(t) >= need > suffix(t + 1); s_res = {t, suffix(t + 1)} ({0, 0} if the
+// histogram holds fewer than `need`, which consistent inputs never do).  Ends with a barrier.
+template <int NB, int NT>
 __device__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_res) {
-  constexpr int BPT = NB >= kTk ? NB / kTk : 1;
+  constexpr int W = NT / kWave;
+  constexpr int BPT = NB >= NT ? NB / NT : 1;
   constexpr int ACTIVE = NB / BPT;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
+  if (tid == 0) {
+    s_res[0] = 0;
+    s_res[1] = 0;
+  }
   int h[BPT];
   int s = 0;
 #pragma unroll
@@ -127,7 +133,8 @@ __device__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_re
   if (lane == 0) s_wtot[w] = x;
   __syncthreads();
   int after = 0;
-  for (int v = w + 1; v < kTkWaves; ++v) after += s_wtot[v];
+#pragma unroll
+  for (int v = 0; v < W; ++v) after += v > w ? s_wtot[v] : 0;
   const int suf = x + after;
   const int suf_next = suf - s;
   if (tid < ACTIVE && suf >= need && suf_next < need) {
@@ -145,8 +152,9 @@ __device__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_re
   __syncthreads();
 }
 
+template <int NT>
 __device__ __forceinline__ void zero_lds(int* p, int n) {
-  for (int i = threadIdx.x; i < n; i += kTk) p[i] = 0;
+  for (int i = threadIdx.x; i < n; i += NT) p[i] = 0;
 }
 
 // Output write guarded to the row's 2048 entries (inputs that break the contract -- e.g. a
@@ -174,160 +182,291 @@ __device__ __forceinline__ int pt_row_of(int row, const int32_t* cu, int n_req) 
   return lo;
 }
 
-// LDS of the single / merge kernels.
-struct TopkLds {
-  int hist[kBins];
-  uint32_t ckey[kCapC];
-  int cidx[kCapC];
-  int2 scan[2 * kTkWaves];
-  int wtot[kTkWaves];
-  int red[kTkWaves];
-  int res[2];
+// Threshold facts of a row from its pass-1 histogram: fast path, digit t1, tokens above t1.
+struct Meta {
+  bool fast;
+  uint32_t t1;
+  int above1;
+  int pos;
 };
 
-// Pass 1 over [begin, end): LDS histogram of key[31:20] of nonzero tokens (zeros are added to
-// the zero bin once); returns positives / zeros of the range (block-uniform).
-template <bool kVec>
+template <int NT>
+__device__ Meta row_meta(const int* hist_lds, int pos, int zeros, int* s_wtot, int* s_res) {
+  Meta m;
+  m.pos = pos;
+  m.fast = pos <= kTopK && pos + zeros >= kTopK;
+  m.t1 = 0;
+  m.above1 = pos;
+  if (!m.fast) {
+    find_threshold<kBins, NT>(hist_lds, kTopK, s_wtot, s_res);
+    m.t1 = static_cast<uint32_t>(s_res[0]);
+    m.above1 = s_res[1];
+  }
+  return m;
+}
+
+// Pass 1 over [begin, end) of the row into an LDS histogram (zeros counted, not binned);
+// returns the range's positive / zero counts (block-uniform).
+template <bool kVec, int NT>
 __device__ void pass_hist(const RowSrc& r, int begin, int end, int* hist, int* s_red, int& pos, int& zeros) {
   RowSrc rr = r;
   rr.len = end;
   int zc = 0, pc = 0;
-  for (int base = begin; base < end; base += kStep) {
-    uint32_t k[4];
-    const uint32_t valid = load_keys4<kVec>(rr, base + static_cast<int>(threadIdx.x) * 4, k);
+  for (int b = begin + static_cast<int>(threadIdx.x) * 4; b < end; b += NT * 4 * kUnroll) {
+    uint32_t k[kUnroll][4];
+    uint32_t v[kUnroll];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if ((valid >> j) & 1u) {
-        if (k[j] == kZeroKey) {
-          ++zc;
-        } else {
-          pc += k[j] > kZeroKey;
-          atomicAdd(&hist[k[j] >> 20], 1);
+    for (int u = 0; u < kUnroll; ++u) v[u] = load_keys4<kVec>(rr, b + u * NT * 4, k[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if ((v[u] >> j) & 1u) {
+          if (k[u][j] == kZeroKey) {
+            ++zc;
+          } else {
+            pc += k[u][j] > kZeroKey;
+            atomicAdd(&hist[k[u][j] >> 20], 1);
+          }
         }
       }
     }
   }
-  pos = block_sum(pc, s_red);
-  zeros = block_sum(zc, s_red);
+  pos = block_sum<NT>(pc, s_red);
+  zeros = block_sum<NT>(zc, s_red);
 }
 
-// Ordered emission over [begin, end) of the row for a fixed threshold key `thr`:
-//  cond(key) selects the tokens that may be above the threshold (all of them, or digit == t1);
-//  keys > thr go to dst[gt_base + rank], keys == thr with tie rank < remaining go to
-//  dst[tie_base + rank].  gt_off / tie_off: ranks already used by earlier ranges.
-template <bool kVec, typename Cond>
-__device__ void emit_range(const RowSrc& r, int begin, int end, Cond cond, uint32_t thr, int gt_base, int tie_base,
-                           int remaining, int gt_off, int tie_off, const PtRow& pt, int32_t* dst, int2* s_scan) {
+// Candidate staging of a CTA: certain tokens (A) and threshold-bin candidates (C).
+struct Stage {
+  int* a;         // token indices, capacity cap_a
+  uint32_t* ck;   // candidate keys, capacity cap_c
+  int* ci;        // candidate tokens
+  int* n_a;       // LDS counters
+  int* n_c;
+  int cap_a;
+  int cap_c;
+};
+
+// Unordered collection over [begin, end): A = keys above bin t1 (fast path: positive keys),
+// C = keys in bin t1 (none on the fast path).  Wave-aggregated LDS atomics give positions.
+template <bool kVec, int NT>
+__device__ void collect(const RowSrc& r, int begin, int end, const Meta& m, const Stage& st) {
   RowSrc rr = r;
   rr.len = end;
-  int gt_pos = gt_off, tie_pos = tie_off;
-  int parity = 0;
-  for (int base = begin; base < end; base += kStep) {
-    const int i0 = base + static_cast<int>(threadIdx.x) * 4;
-    uint32_t k[4];
-    const uint32_t valid = load_keys4<kVec>(rr, i0, k);
-    int ng = 0, ne = 0;
-    bool g[4], e[4];
+  for (int b = begin + static_cast<int>(threadIdx.x) * 4; b < end; b += NT * 4 * kUnroll) {
+    uint32_t k[kUnroll][4];
+    uint32_t v[kUnroll];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool v = ((valid >> j) & 1u) && cond(k[j]);
-      g[j] = v && k[j] > thr;
-      e[j] = v && k[j] == thr;
-      ng += g[j];
-      ne += e[j];
-    }
-    int pg, pe, tg, te;
-    block_prefix2(ng, ne, pg, pe, tg, te, s_scan, parity);
-    parity ^= 1;
-    pg += gt_pos;
-    pe += tie_pos;
+    for (int u = 0; u < kUnroll; ++u) v[u] = load_keys4<kVec>(rr, b + u * NT * 4, k[u]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (g[j]) put(dst, gt_base + pg, pt[i0 + j]);
-      if (e[j] && pe < remaining) put(dst, tie_base + pe, pt[i0 + j]);
-      pg += g[j];
-      pe += e[j];
+    for (int u = 0; u < kUnroll; ++u) {
+      int na = 0, nc = 0;
+      bool fa[4], fc[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool valid = (v[u] >> j) & 1u;
+        const uint32_t d = k[u][j] >> 20;
+        fa[j] = valid && (m.fast ? k[u][j] > kZeroKey : d > m.t1);
+        fc[j] = valid && !m.fast && d == m.t1;
+        na += fa[j];
+        nc += fc[j];
+      }
+      int ta, tc;
+      int pa = wave_prefix_small(na, ta);
+      int pc = wave_prefix_small(nc, tc);
+      if (ta | tc) {  // wave-uniform
+        int base_a = 0, base_c = 0;
+        if (lane_id() == 0) {
+          if (ta) base_a = atomicAdd(st.n_a, ta);
+          if (tc) base_c = atomicAdd(st.n_c, tc);
+        }
+        base_a = __shfl(base_a, 0);
+        base_c = __shfl(base_c, 0);
+        const int i0 = b + u * NT * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (fa[j]) {
+            const int idx = base_a + pa++;
+            if (idx < st.cap_a) st.a[idx] = i0 + j;
+          }
+          if (fc[j]) {
+            const int idx = base_c + pc++;
+            if (idx < st.cap_c) {
+              st.ck[idx] = k[u][j];
+              st.ci[idx] = i0 + j;
+            }
+          }
+        }
+      }
     }
-    gt_pos += tg;
-    tie_pos += te;
   }
 }
 
-// Resolves the exact threshold among the LDS candidates C (all with digit t1, in token order)
-// and emits them.  above1 = tokens already emitted (digit > t1); need1 = 2048 - above1.
-__device__ void resolve_lds(TopkLds& L, int n_c, uint32_t t1, int above1, const PtRow& pt, int32_t* dst) {
-  const int need1 = kTopK - above1;
-  zero_lds(L.hist, kBins);
+// Radix select over LDS members: the key `thr` such that `need` members have key >= thr and the
+// number of members with key > thr (returned in above).  key_of(e) / member(e) index 0..n-1.
+template <int NT, typename KeyOf, typename Member>
+__device__ uint32_t radix_select(int n, int need, KeyOf key_of, Member member, int* hist, int* s_wtot, int* s_res,
+                                 int& above) {
+  zero_lds<NT>(hist, kBins);
   __syncthreads();
-  for (int e = threadIdx.x; e < n_c; e += kTk) atomicAdd(&L.hist[(L.ckey[e] >> 8) & 0xFFFu], 1);
+  for (int e = threadIdx.x; e < n; e += NT)
+    if (member(e)) atomicAdd(&hist[key_of(e) >> 20], 1);
   __syncthreads();
-  find_threshold<kBins>(L.hist, need1, L.wtot, L.res);
-  const uint32_t prefix24 = (t1 << 12) | static_cast<uint32_t>(L.res[0]);
-  const int need2 = need1 - L.res[1];
-  zero_lds(L.hist, 256);
+  find_threshold<kBins, NT>(hist, need, s_wtot, s_res);
+  const uint32_t d1 = static_cast<uint32_t>(s_res[0]);
+  int ab = s_res[1];
+  const int need2 = need - s_res[1];
+  zero_lds<NT>(hist, kBins);
   __syncthreads();
-  for (int e = threadIdx.x; e < n_c; e += kTk) {
-    const uint32_t key = L.ckey[e];
-    if ((key >> 8) == prefix24) atomicAdd(&L.hist[key & 0xFFu], 1);
+  for (int e = threadIdx.x; e < n; e += NT) {
+    if (!member(e)) continue;
+    const uint32_t k = key_of(e);
+    if ((k >> 20) == d1) atomicAdd(&hist[(k >> 8) & 0xFFFu], 1);
   }
   __syncthreads();
-  find_threshold<256>(L.hist, need2, L.wtot, L.res);
-  const uint32_t thr = (prefix24 << 8) | static_cast<uint32_t>(L.res[0]);
-  const int remaining = need2 - L.res[1];
+  find_threshold<kBins, NT>(hist, need2, s_wtot, s_res);
+  const uint32_t p24 = (d1 << 12) | static_cast<uint32_t>(s_res[0]);
+  ab += s_res[1];
+  const int need3 = need2 - s_res[1];
+  zero_lds<NT>(hist, 256);
+  __syncthreads();
+  for (int e = threadIdx.x; e < n; e += NT) {
+    if (!member(e)) continue;
+    const uint32_t k = key_of(e);
+    if ((k >> 8) == p24) atomicAdd(&hist[k & 0xFFu], 1);
+  }
+  __syncthreads();
+  find_threshold<256, NT>(hist, need3, s_wtot, s_res);
+  above = ab + s_res[1];
+  return (p24 << 8) | static_cast<uint32_t>(s_res[0]);
+}
+
+struct ResolveLds {
+  int hist[kBins];
+  uint32_t ck[kCapC];
+  int ci[kCapC];
+  int scan[2 * (kTk / kWave)];
+  int wtot[kTk / kWave];
+  int red[kTk / kWave];
+  int res[2];
+  int misc[4];
+};
+
+// Resolves the LDS candidates (all in bin t1, unordered) of a row whose above1 tokens above
+// bin t1 are already in dst[0, above1).
+__device__ void resolve_lds(ResolveLds& L, int n_c, int above1, const PtRow& pt, int32_t* dst) {
+  const int need1 = kTopK - above1;
+  int gt;
+  const uint32_t thr = radix_select<kTk>(
+      n_c, need1, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt);
+  const int remaining = need1 - gt;
   const int tie_base = kTopK - remaining;
+  // ties at thr: all of them, unless there are more than `remaining` -- then the lowest tokens,
+  // found by a radix select over ~token among the ties.
+  int n_eq = 0;
+  for (int e = threadIdx.x; e < n_c; e += kTk) n_eq += L.ck[e] == thr;
+  n_eq = block_sum<kTk>(n_eq, L.red);
+  uint32_t idx_thr = 0;  // ties kept: ~token >= idx_thr
+  if (n_eq > remaining) {
+    int unused;
+    idx_thr = radix_select<kTk>(
+        n_c, remaining, [&](int e) { return ~static_cast<uint32_t>(L.ci[e]); },
+        [&](int e) { return L.ck[e] == thr; }, L.hist, L.wtot, L.res, unused);
+  }
   int gt_pos = 0, tie_pos = 0, parity = 0;
   for (int base = 0; base < n_c; base += kTk) {
     const int e = base + static_cast<int>(threadIdx.x);
-    const uint32_t key = e < n_c ? L.ckey[e] : 0u;
+    const uint32_t key = e < n_c ? L.ck[e] : 0u;
     const bool g = e < n_c && key > thr;
-    const bool q = e < n_c && key == thr;
-    int pg, pe, tg, te;
-    block_prefix2(g, q, pg, pe, tg, te, L.scan, parity);
+    const bool q = e < n_c && key == thr && ~static_cast<uint32_t>(L.ci[e]) >= idx_thr;
+    int tg, tq;
+    const int pg = block_prefix<kTk>(g, tg, L.scan, parity);
     parity ^= 1;
-    pg += gt_pos;
-    pe += tie_pos;
-    if (g) put(dst, above1 + pg, pt[L.cidx[e]]);
-    if (q && pe < remaining) put(dst, tie_base + pe, pt[L.cidx[e]]);
+    const int pq = block_prefix<kTk>(q, tq, L.scan, parity);
+    parity ^= 1;
+    if (g) put(dst, above1 + gt_pos + pg, pt[L.ci[e]]);
+    if (q) put(dst, tie_base + tie_pos + pq, pt[L.ci[e]]);
     gt_pos += tg;
-    tie_pos += te;
+    tie_pos += tq;
   }
 }
 
-// Threshold resolution by re-reading the row (candidates did not fit): digit passes over the
-// tokens of bin t1, then the ordered emission of those above / at the threshold.
+// Ordered scan of the row for the first `remaining` tokens with key == thr that pass `cond`
+// (fast path: the zeros; rescan: the ties), written to dst[base + rank]; stops once enough
+// were found unless gt is set.  gt: also write the keys > thr that pass cond to
+// dst[gt_base + rank] (rescan only; then the whole row is scanned).
+template <bool kVec, typename Cond>
+__device__ void ordered_scan(const RowSrc& r, Cond cond, uint32_t thr, bool gt, int gt_base, int base, int remaining,
+                             const PtRow& pt, int32_t* dst, int* s_scan) {
+  int taken = 0, gt_pos = 0, parity = 0;
+  for (int b0 = 0; b0 < r.len && (gt || taken < remaining); b0 += kTk * 4) {
+    const int i0 = b0 + static_cast<int>(threadIdx.x) * 4;
+    uint32_t k[4];
+    const uint32_t v = load_keys4<kVec>(r, i0, k);
+    int ne = 0, ng = 0;
+    bool e[4], g[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool c = ((v >> j) & 1u) && cond(k[j]);
+      e[j] = c && k[j] == thr;
+      g[j] = gt && c && k[j] > thr;
+      ne += e[j];
+      ng += g[j];
+    }
+    int te, tg;
+    int pe = block_prefix<kTk>(ne, te, s_scan, parity);
+    parity ^= 1;
+    int pg = block_prefix<kTk>(ng, tg, s_scan, parity);
+    parity ^= 1;
+    pe += taken;
+    pg += gt_pos;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (e[j] && pe < remaining) put(dst, base + pe, pt[i0 + j]);
+      if (g[j]) put(dst, gt_base + pg, pt[i0 + j]);
+      pe += e[j];
+      pg += g[j];
+    }
+    taken += te;
+    gt_pos += tg;
+  }
+}
+
+// Threshold resolution by re-reading the row (candidates did not fit in LDS): digit passes over
+// the tokens of bin t1, then an ordered emission of those above / at the threshold.
 template <bool kVec>
-__device__ void resolve_rescan(TopkLds& L, const RowSrc& r, uint32_t t1, int above1, const PtRow& pt,
+__device__ void resolve_rescan(ResolveLds& L, const RowSrc& r, uint32_t t1, int above1, const PtRow& pt,
                                int32_t* dst) {
   const int need1 = kTopK - above1;
-  zero_lds(L.hist, kBins);
+  zero_lds<kTk>(L.hist, kBins);
   __syncthreads();
-  for (int base = 0; base < r.len; base += kStep) {
+  for (int b = static_cast<int>(threadIdx.x) * 4; b < r.len; b += kTk * 4) {
     uint32_t k[4];
-    const uint32_t valid = load_keys4<kVec>(r, base + static_cast<int>(threadIdx.x) * 4, k);
+    const uint32_t v = load_keys4<kVec>(r, b, k);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (((valid >> j) & 1u) && (k[j] >> 20) == t1) atomicAdd(&L.hist[(k[j] >> 8) & 0xFFFu], 1);
+      if (((v >> j) & 1u) && (k[j] >> 20) == t1) atomicAdd(&L.hist[(k[j] >> 8) & 0xFFFu], 1);
   }
   __syncthreads();
-  find_threshold<kBins>(L.hist, need1, L.wtot, L.res);
+  find_threshold<kBins, kTk>(L.hist, need1, L.wtot, L.res);
   const uint32_t prefix24 = (t1 << 12) | static_cast<uint32_t>(L.res[0]);
   const int need2 = need1 - L.res[1];
-  zero_lds(L.hist, 256);
+  zero_lds<kTk>(L.hist, 256);
   __syncthreads();
-  for (int base = 0; base < r.len; base += kStep) {
+  for (int b = static_cast<int>(threadIdx.x) * 4; b < r.len; b += kTk * 4) {
     uint32_t k[4];
-    const uint32_t valid = load_keys4<kVec>(r, base + static_cast<int>(threadIdx.x) * 4, k);
+    const uint32_t v = load_keys4<kVec>(r, b, k);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (((valid >> j) & 1u) && (k[j] >> 8) == prefix24) atomicAdd(&L.hist[k[j] & 0xFFu], 1);
+      if (((v >> j) & 1u) && (k[j] >> 8) == prefix24) atomicAdd(&L.hist[k[j] & 0xFFu], 1);
   }
   __syncthreads();
-  find_threshold<256>(L.hist, need2, L.wtot, L.res);
+  find_threshold<256, kTk>(L.hist, need2, L.wtot, L.res);
   const uint32_t thr = (prefix24 << 8) | static_cast<uint32_t>(L.res[0]);
   const int remaining = need2 - L.res[1];
-  emit_range<kVec>(
-      r, 0, r.len, [t1](uint32_t k) { return (k >> 20) == t1; }, thr, above1, kTopK - remaining, remaining, 0, 0, pt,
-      dst, L.scan);
+  ordered_scan<kVec>(
+      r, [t1](uint32_t k) { return (k >> 20) == t1; }, thr, true, above1, kTopK - remaining, remaining, pt, dst,
+      L.scan);
 }
 
 struct TopkArgs {
@@ -344,13 +483,13 @@ struct TopkArgs {
   const int32_t* cu;
   int n_req;
   int32_t* out;
-  // split / pre workspace
   int S;
-  int32_t* ghist;   // [rows][kBins]          (pass 1)
+  int32_t* ghist;   // [rows][kBins]  pass-1 histogram
   int32_t* gcnt;    // [rows][2] = (positives, zeros)
-  int32_t* cnt_ac;  // [rows][S][2] = (|A_s|, |C_s|)
-  int32_t* list_a;  // [rows][S][kTopK]
-  int32_t* list_c;  // [rows][S][kCapSlice][2] = (key, token)
+  int32_t* ctr;     // per row: output positions used by the collect CTAs (row stride ctr_stride)
+  int64_t ctr_stride;
+  int32_t* c_cnt;   // [rows][S] candidates found per slice
+  int32_t* c_list;  // [rows][S][kCapSlice][2] = (key, token)
 };
 
 __device__ __forceinline__ RowSrc row_src(const TopkArgs& a, int row, int len) {
@@ -373,24 +512,26 @@ __device__ __forceinline__ PtRow pt_row(const TopkArgs& a, int row) {
   return p;
 }
 
+template <int NT>
 __device__ __forceinline__ void copy_short_row(const PtRow& pt, int32_t* dst, int len) {
-  for (int i = threadIdx.x; i < kTopK; i += kTk) dst[i] = i < len ? pt[i] : -1;
+  for (int i = threadIdx.x; i < kTopK; i += NT) dst[i] = i < len ? pt[i] : -1;
 }
 
+// ---------------------------------------------------------------------------------------------
 // One CTA per row.  kPre: pass 1 (histogram + counts) comes from a.ghist / a.gcnt.
 template <bool kVec, bool kPre>
 __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
-  __shared__ TopkLds L;
+  __shared__ ResolveLds L;
+  __shared__ int s_a[kTopK];
   const int row = blockIdx.x;
   const int len = row_len(a, row);
   const PtRow pt = pt_row(a, row);
   int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
   if (len <= kTopK) {
-    copy_short_row(pt, dst, len);
+    copy_short_row<kTk>(pt, dst, len);
     return;
   }
   const RowSrc r = row_src(a, row, len);
-
   int pos, zeros;
   if constexpr (kPre) {
     const int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
@@ -399,82 +540,53 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
     zeros = a.gcnt[2 * row + 1];
     __syncthreads();
   } else {
-    zero_lds(L.hist, kBins);
+    zero_lds<kTk>(L.hist, kBins);
     __syncthreads();
-    pass_hist<kVec>(r, 0, len, L.hist, L.red, pos, zeros);
+    pass_hist<kVec, kTk>(r, 0, len, L.hist, L.red, pos, zeros);
     if (threadIdx.x == 0 && zeros) L.hist[kZeroBin] += zeros;
     __syncthreads();
   }
-
-  if (pos <= kTopK && pos + zeros >= kTopK) {
-    // Threshold is +0: every positive token plus the lowest-index zeros.
-    const int remaining = kTopK - pos;
-    emit_range<kVec>(
-        r, 0, len, [](uint32_t) { return true; }, kZeroKey, 0, pos, remaining, 0, 0, pt, dst, L.scan);
-    return;
-  }
-  find_threshold<kBins>(L.hist, kTopK, L.wtot, L.res);
-  const uint32_t t1 = static_cast<uint32_t>(L.res[0]);
-  const int above1 = L.res[1];
-
-  // Pass 2: list A straight to the output, list C into LDS, both in token order.
-  int a_pos = 0, c_pos = 0, parity = 0;
-  for (int base = 0; base < len; base += kStep) {
-    const int i0 = base + static_cast<int>(threadIdx.x) * 4;
-    uint32_t k[4];
-    const uint32_t valid = load_keys4<kVec>(r, i0, k);
-    int na = 0, nc = 0;
-    bool fa[4], fc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool v = (valid >> j) & 1u;
-      fa[j] = v && (k[j] >> 20) > t1;
-      fc[j] = v && (k[j] >> 20) == t1;
-      na += fa[j];
-      nc += fc[j];
-    }
-    int pa, pc, ta, tc;
-    block_prefix2(na, nc, pa, pc, ta, tc, L.scan, parity);
-    parity ^= 1;
-    pa += a_pos;
-    pc += c_pos;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (fa[j]) put(dst, pa, pt[i0 + j]);
-      if (fc[j] && pc < kCapC) {
-        L.ckey[pc] = k[j];
-        L.cidx[pc] = i0 + j;
-      }
-      pa += fa[j];
-      pc += fc[j];
-    }
-    a_pos += ta;
-    c_pos += tc;
-  }
+  const Meta m = row_meta<kTk>(L.hist, pos, zeros, L.wtot, L.res);
+  if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
   __syncthreads();
-  if (c_pos <= kCapC) resolve_lds(L, c_pos, t1, above1, pt, dst);
-  else resolve_rescan<kVec>(L, r, t1, above1, pt, dst);
+  Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
+  collect<kVec, kTk>(r, 0, len, m, st);
+  __syncthreads();
+  const int n_a = min(L.misc[0], kTopK);
+  const int n_c = L.misc[1];
+  for (int i = threadIdx.x; i < n_a; i += kTk) put(dst, i, pt[s_a[i]]);
+  if (m.fast) {
+    ordered_scan<kVec>(
+        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
+  } else if (n_c <= kCapC) {
+    resolve_lds(L, n_c, m.above1, pt, dst);
+  } else {
+    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Split variant.  Slices are whole kStep blocks; CTAs are slice-major (blockIdx = s * rows + row)
-// so the live slices of consecutive rows spread over the XCDs.
+// Split variant.  Slices are multiples of 1024 tokens; CTAs are slice-major (blockIdx = s *
+// rows + row), so the slices of consecutive rows spread over the XCDs.
 __device__ __forceinline__ int slice_len(int len, int S) {
   const int per = (len + S - 1) / S;
-  return (per + kStep - 1) / kStep * kStep;
+  return (per + 1023) / 1024 * 1024;
 }
 
-__global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ ghist, int32_t* __restrict__ gcnt) {
+// Zeroes the pass-1 histogram, counts and output counters of the split path.
+__global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ ghist, int32_t* __restrict__ gcnt,
+                                                        int32_t* __restrict__ ctr, int64_t ctr_stride) {
   const int row = blockIdx.x;
   int4* g = reinterpret_cast<int4*>(ghist + static_cast<int64_t>(row) * kBins);
   for (int i = threadIdx.x; i < kBins / 4; i += 256) g[i] = make_int4(0, 0, 0, 0);
   if (threadIdx.x < 2) gcnt[2 * row + threadIdx.x] = 0;
+  if (threadIdx.x == 2) ctr[row * ctr_stride] = 0;
 }
 
 template <bool kVec>
-__global__ __launch_bounds__(kTk) void topk_split_hist_kernel(const TopkArgs a) {
+__global__ __launch_bounds__(kTs) void topk_split_hist_kernel(const TopkArgs a) {
   __shared__ int hist[kBins];
-  __shared__ int red[kTkWaves];
+  __shared__ int red[kTs / kWave];
   const int row = blockIdx.x % a.rows;
   const int s = blockIdx.x / a.rows;
   const int len = row_len(a, row);
@@ -483,12 +595,12 @@ __global__ __launch_bounds__(kTk) void topk_split_hist_kernel(const TopkArgs a) 
   const int begin = s * sl;
   if (begin >= len) return;
   const int end = min(begin + sl, len);
-  zero_lds(hist, kBins);
+  zero_lds<kTs>(hist, kBins);
   __syncthreads();
   int pos, zeros;
-  pass_hist<kVec>(row_src(a, row, len), begin, end, hist, red, pos, zeros);
+  pass_hist<kVec, kTs>(row_src(a, row, len), begin, end, hist, red, pos, zeros);
   int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
-  for (int i = threadIdx.x; i < kBins; i += kTk) {
+  for (int i = threadIdx.x; i < kBins; i += kTs) {
     const int c = hist[i] + (i == kZeroBin ? zeros : 0);
     if (c) atomicAdd(&gh[i], c);
   }
@@ -498,13 +610,17 @@ __global__ __launch_bounds__(kTk) void topk_split_hist_kernel(const TopkArgs a) 
   }
 }
 
-// Per slice: ordered compaction into list A (certain) and list C (threshold candidates).
+// Per slice: unordered collection; A goes straight to the output through one global atomic
+// per CTA, C is stored in the slice's candidate list.
 template <bool kVec>
-__global__ __launch_bounds__(kTk) void topk_split_compact_kernel(const TopkArgs a) {
+__global__ __launch_bounds__(kTs) void topk_split_collect_kernel(const TopkArgs a) {
   __shared__ int hist[kBins];
-  __shared__ int2 scan[2 * kTkWaves];
-  __shared__ int wtot[kTkWaves];
-  __shared__ int res[2];
+  __shared__ int s_a[kTopK];
+  __shared__ uint32_t s_ck[kCapSlice];
+  __shared__ int s_ci[kCapSlice];
+  __shared__ int s_wtot[kTs / kWave];
+  __shared__ int s_res[2];
+  __shared__ int s_n[3];
   const int row = blockIdx.x % a.rows;
   const int s = blockIdx.x / a.rows;
   const int len = row_len(a, row);
@@ -516,145 +632,98 @@ __global__ __launch_bounds__(kTk) void topk_split_compact_kernel(const TopkArgs 
   const int pos = a.gcnt[2 * row];
   const int zeros = a.gcnt[2 * row + 1];
   const bool fast = pos <= kTopK && pos + zeros >= kTopK;
-  uint32_t t1 = 0;
-  int cap_c = kCapSlice;
-  if (fast) {
-    cap_c = min(kCapSlice, kTopK - pos);  // only the first `remaining` zeros can be selected
-  } else {
+  if (!fast) {
     const int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
-    for (int i = threadIdx.x; i < kBins; i += kTk) hist[i] = gh[i];
-    __syncthreads();
-    find_threshold<kBins>(hist, kTopK, wtot, res);
-    t1 = static_cast<uint32_t>(res[0]);
+    for (int i = threadIdx.x; i < kBins; i += kTs) hist[i] = gh[i];
   }
-  const int64_t slot = static_cast<int64_t>(row) * a.S + s;
-  int32_t* la = a.list_a + slot * kTopK;
-  int32_t* lc = a.list_c + slot * kCapSlice * 2;
-  RowSrc r = row_src(a, row, end);
-  int a_pos = 0, c_pos = 0, parity = 0;
-  for (int base = begin; base < end; base += kStep) {
-    const int i0 = base + static_cast<int>(threadIdx.x) * 4;
-    uint32_t k[4];
-    const uint32_t valid = load_keys4<kVec>(r, i0, k);
-    int na = 0, nc = 0;
-    bool fa[4], fc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool v = (valid >> j) & 1u;
-      fa[j] = v && (fast ? k[j] > kZeroKey : (k[j] >> 20) > t1);
-      fc[j] = v && (fast ? k[j] == kZeroKey : (k[j] >> 20) == t1);
-      na += fa[j];
-      nc += fc[j];
-    }
-    int pa, pc, ta, tc;
-    block_prefix2(na, nc, pa, pc, ta, tc, scan, parity);
-    parity ^= 1;
-    pa += a_pos;
-    pc += c_pos;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (fa[j] && pa < kTopK) la[pa] = i0 + j;
-      if (fc[j] && pc < cap_c) {
-        lc[2 * pc] = static_cast<int>(k[j]);
-        lc[2 * pc + 1] = i0 + j;
-      }
-      pa += fa[j];
-      pc += fc[j];
-    }
-    a_pos += ta;
-    c_pos += tc;
-  }
+  if (threadIdx.x == 0) s_n[0] = s_n[1] = 0;
+  __syncthreads();
+  const Meta m = row_meta<kTs>(hist, pos, zeros, s_wtot, s_res);
+  Stage st{s_a, s_ck, s_ci, &s_n[0], &s_n[1], kTopK, kCapSlice};
+  collect<kVec, kTs>(row_src(a, row, len), begin, end, m, st);
+  __syncthreads();
+  const int n_a = min(s_n[0], kTopK);
+  const int n_c = s_n[1];
   if (threadIdx.x == 0) {
-    a.cnt_ac[2 * slot] = a_pos;
-    a.cnt_ac[2 * slot + 1] = c_pos;
+    s_n[2] = n_a ? atomicAdd(a.ctr + row * a.ctr_stride, n_a) : 0;
+    a.c_cnt[static_cast<int64_t>(row) * a.S + s] = n_c;
+  }
+  __syncthreads();
+  const PtRow pt = pt_row(a, row);
+  int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
+  const int base = s_n[2];
+  for (int i = threadIdx.x; i < n_a; i += kTs) put(dst, base + i, pt[s_a[i]]);
+  int32_t* lc = a.c_list + (static_cast<int64_t>(row) * a.S + s) * kCapSlice * 2;
+  const int m_c = min(n_c, kCapSlice);
+  for (int i = threadIdx.x; i < m_c; i += kTs) {
+    lc[2 * i] = static_cast<int>(s_ck[i]);
+    lc[2 * i + 1] = s_ci[i];
   }
 }
 
-// One CTA per row: merges the slices' lists, resolves the threshold, writes the output.
+// One CTA per row: merges the slices' candidates and resolves the threshold (or, on the fast
+// path, takes the lowest-index zeros).
 template <bool kVec>
 __global__ __launch_bounds__(kTk) void topk_split_finish_kernel(const TopkArgs a) {
-  __shared__ TopkLds L;
-  __shared__ int s_pre[2 * kMaxSplit + 2];
+  __shared__ ResolveLds L;
+  __shared__ int s_off[kMaxSplit + 1];
   const int row = blockIdx.x;
   const int len = row_len(a, row);
   const PtRow pt = pt_row(a, row);
   int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
   if (len <= kTopK) {
-    copy_short_row(pt, dst, len);
+    copy_short_row<kTk>(pt, dst, len);
     return;
   }
-  const int sl = slice_len(len, a.S);
-  const int n_sl = (len + sl - 1) / sl;
+  const RowSrc r = row_src(a, row, len);
   const int pos = a.gcnt[2 * row];
   const int zeros = a.gcnt[2 * row + 1];
-  const bool fast = pos <= kTopK && pos + zeros >= kTopK;
-  const int32_t* cnt = a.cnt_ac + static_cast<int64_t>(row) * a.S * 2;
-  if (threadIdx.x == 0) {
-    // Exclusive prefixes of |A_s| and |C_s| over slices; overflow flag at the end.
-    int pa = 0, pc = 0, over = 0;
-    for (int s = 0; s < n_sl; ++s) {
-      s_pre[2 * s] = pa;
-      s_pre[2 * s + 1] = pc;
-      pa += cnt[2 * s];
-      const int c = cnt[2 * s + 1];
-      over |= !fast && c > kCapSlice;
-      pc += c;
-    }
-    s_pre[2 * n_sl] = pa;
-    s_pre[2 * n_sl + 1] = over || (!fast && pc > kCapC) ? -1 : pc;
-  }
-  __syncthreads();
-  const int n_a = s_pre[2 * n_sl];
-  const int n_c = s_pre[2 * n_sl + 1];
-
-  // List A (already in token order per slice) -> output positions [0, n_a).
-  for (int s = 0; s < n_sl; ++s) {
-    const int32_t* la = a.list_a + (static_cast<int64_t>(row) * a.S + s) * kTopK;
-    const int m = min(cnt[2 * s], kTopK);
-    const int off = s_pre[2 * s];
-    for (int i = threadIdx.x; i < m; i += kTk) put(dst, off + i, pt[la[i]]);
-  }
-  if (fast) {
-    // Ties are zeros: the first (2048 - pos) of the slices' zero lists, in slice order.
-    const int remaining = kTopK - pos;
-    for (int s = 0; s < n_sl; ++s) {
-      const int32_t* lc = a.list_c + (static_cast<int64_t>(row) * a.S + s) * kCapSlice * 2;
-      const int off = s_pre[2 * s + 1];
-      const int m = min(cnt[2 * s + 1], kCapSlice);
-      for (int i = threadIdx.x; i < m; i += kTk)
-        if (off + i < remaining) put(dst, pos + off + i, pt[lc[2 * i + 1]]);
-    }
+  if (pos <= kTopK && pos + zeros >= kTopK) {
+    ordered_scan<kVec>(
+        r, [](uint32_t) { return true; }, kZeroKey, false, 0, pos, kTopK - pos, pt, dst, L.scan);
     return;
   }
-  // Non-fast: t1 from the global histogram (same as the compact kernels computed).
   const int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
   for (int i = threadIdx.x; i < kBins; i += kTk) L.hist[i] = gh[i];
   __syncthreads();
-  find_threshold<kBins>(L.hist, kTopK, L.wtot, L.res);
-  const uint32_t t1 = static_cast<uint32_t>(L.res[0]);
-  const int above1 = L.res[1];
-  if (n_c >= 0) {
+  const Meta m = row_meta<kTk>(L.hist, pos, zeros, L.wtot, L.res);
+  const int sl = slice_len(len, a.S);
+  const int n_sl = (len + sl - 1) / sl;
+  if (threadIdx.x == 0) {
+    int off = 0;
+    bool over = false;
     for (int s = 0; s < n_sl; ++s) {
-      const int32_t* lc = a.list_c + (static_cast<int64_t>(row) * a.S + s) * kCapSlice * 2;
-      const int off = s_pre[2 * s + 1];
-      const int m = cnt[2 * s + 1];
-      for (int i = threadIdx.x; i < m; i += kTk) {
-        L.ckey[off + i] = static_cast<uint32_t>(lc[2 * i]);
-        L.cidx[off + i] = lc[2 * i + 1];
-      }
+      const int c = a.c_cnt[static_cast<int64_t>(row) * a.S + s];
+      s_off[s] = off;
+      over |= c > kCapSlice;
+      off += c;
     }
-    __syncthreads();
-    resolve_lds(L, n_c, t1, above1, pt, dst);
-  } else {
-    resolve_rescan<kVec>(L, row_src(a, row, len), t1, above1, pt, dst);
+    s_off[n_sl] = over || off > kCapC ? -1 : off;
   }
+  __syncthreads();
+  const int n_c = s_off[n_sl];
+  if (n_c < 0) {
+    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
+    return;
+  }
+  for (int s = 0; s < n_sl; ++s) {
+    const int32_t* lc = a.c_list + (static_cast<int64_t>(row) * a.S + s) * kCapSlice * 2;
+    const int off = s_off[s];
+    const int cnt = (s + 1 < n_sl ? s_off[s + 1] : n_c) - off;
+    for (int i = threadIdx.x; i < cnt; i += kTk) {
+      L.ck[off + i] = static_cast<uint32_t>(lc[2 * i]);
+      L.ci[off + i] = lc[2 * i + 1];
+    }
+  }
+  __syncthreads();
+  resolve_lds(L, n_c, m.above1, pt, dst);
 }
 
 int split_count(int64_t rows, int64_t width, int max_splits, int n_cu) {
   if (rows <= 0) return 1;
-  int64_t s = (width + 2 * kStep - 1) / (2 * kStep);  // >= 8192 tokens per slice
+  int64_t s = (width + 4095) / 4096;  // >= 4096 tokens per slice
   s = s < 1 ? 1 : s;
-  const int64_t by_cu = n_cu / rows;
+  const int64_t by_cu = (2 * static_cast<int64_t>(n_cu)) / rows;
   s = s < by_cu ? s : by_cu;
   const int64_t cap = max_splits < kMaxSplit ? max_splits : kMaxSplit;
   s = s < cap ? s : cap;
@@ -662,7 +731,7 @@ int split_count(int64_t rows, int64_t width, int max_splits, int n_cu) {
 }
 
 struct WsLayout {
-  size_t ghist, gcnt, cnt_ac, list_a, list_c, total;
+  size_t ghist, gcnt, ctr, c_cnt, c_list, total;
 };
 
 WsLayout ws_layout(int64_t rows, int S) {
@@ -675,16 +744,16 @@ WsLayout ws_layout(int64_t rows, int S) {
   };
   l.ghist = take(sizeof(int32_t) * rows * kBins);
   l.gcnt = take(sizeof(int32_t) * rows * 2);
-  l.cnt_ac = take(sizeof(int32_t) * rows * S * 2);
-  l.list_a = take(sizeof(int32_t) * rows * S * kTopK);
-  l.list_c = take(sizeof(int32_t) * rows * S * kCapSlice * 2);
+  l.ctr = take(sizeof(int32_t) * rows);
+  l.c_cnt = take(sizeof(int32_t) * rows * S);
+  l.c_list = take(sizeof(int32_t) * rows * S * kCapSlice * 2);
   l.total = off;
   return l;
 }
 
 int topk_common(const float* score, int64_t score_stride, int64_t width, const int16_t* mask, int64_t mask_stride,
                 const int32_t* lengths, int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
-                const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu, const int32_t* pre_hist,
+                const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu, int32_t* pre_hist,
                 void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream, const char* who) {
   DSA_REQUIRE(rows >= 0 && rows <= 0x7FFFFFFF, "%s: rows out of range", who);
   DSA_REQUIRE(width >= 0 && width <= 0x7FFFFFFF, "%s: width out of range", who);
@@ -713,12 +782,17 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
   a.out = out;
   const int S = split_count(rows, width, max_splits, n_cu);
   a.S = S;
-  a.ghist = a.gcnt = a.cnt_ac = a.list_a = a.list_c = nullptr;
+  a.ghist = a.gcnt = a.ctr = a.c_cnt = a.c_list = nullptr;
+  a.ctr_stride = 1;
   const dim3 grid_rows(static_cast<uint32_t>(rows));
 
   if (pre_hist != nullptr) {
-    a.ghist = const_cast<int32_t*>(pre_hist);
-    a.gcnt = const_cast<int32_t*>(pre_hist) + 2 * rows * kBins;
+    // [ghist1 rows*4096 | ghist2 rows*4096 | cnt rows*2]; word 0 of each ghist2 row is the row's
+    // output counter (zeroed by the logits call that built pass 1).
+    a.ghist = pre_hist;
+    a.ctr = pre_hist + rows * kBins;
+    a.ctr_stride = kBins;
+    a.gcnt = pre_hist + 2 * rows * kBins;
   }
   if (S <= 1) {
     if (pre_hist) {
@@ -738,21 +812,21 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
   if (!pre_hist) {
     a.ghist = reinterpret_cast<int32_t*>(ws + l.ghist);
     a.gcnt = reinterpret_cast<int32_t*>(ws + l.gcnt);
+    a.ctr = reinterpret_cast<int32_t*>(ws + l.ctr);
   }
-  a.cnt_ac = reinterpret_cast<int32_t*>(ws + l.cnt_ac);
-  a.list_a = reinterpret_cast<int32_t*>(ws + l.list_a);
-  a.list_c = reinterpret_cast<int32_t*>(ws + l.list_c);
+  a.c_cnt = reinterpret_cast<int32_t*>(ws + l.c_cnt);
+  a.c_list = reinterpret_cast<int32_t*>(ws + l.c_list);
   const dim3 grid_split(static_cast<uint32_t>(rows * S));
   if (!pre_hist) {
-    hipLaunchKernelGGL(topk_zero_kernel, grid_rows, dim3(256), 0, stream, a.ghist, a.gcnt);
-    if (vec) hipLaunchKernelGGL((topk_split_hist_kernel<true>), grid_split, dim3(kTk), 0, stream, a);
-    else hipLaunchKernelGGL((topk_split_hist_kernel<false>), grid_split, dim3(kTk), 0, stream, a);
+    hipLaunchKernelGGL(topk_zero_kernel, grid_rows, dim3(256), 0, stream, a.ghist, a.gcnt, a.ctr, a.ctr_stride);
+    if (vec) hipLaunchKernelGGL((topk_split_hist_kernel<true>), grid_split, dim3(kTs), 0, stream, a);
+    else hipLaunchKernelGGL((topk_split_hist_kernel<false>), grid_split, dim3(kTs), 0, stream, a);
   }
   if (vec) {
-    hipLaunchKernelGGL((topk_split_compact_kernel<true>), grid_split, dim3(kTk), 0, stream, a);
+    hipLaunchKernelGGL((topk_split_collect_kernel<true>), grid_split, dim3(kTs), 0, stream, a);
     hipLaunchKernelGGL((topk_split_finish_kernel<true>), grid_rows, dim3(kTk), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((topk_split_compact_kernel<false>), grid_split, dim3(kTk), 0, stream, a);
+    hipLaunchKernelGGL((topk_split_collect_kernel<false>), grid_split, dim3(kTs), 0, stream, a);
     hipLaunchKernelGGL((topk_split_finish_kernel<false>), grid_rows, dim3(kTk), 0, stream, a);
   }
   return check_launch(who);
@@ -772,9 +846,8 @@ extern "C" size_t dsa_topk_workspace_bytes(int64_t rows, int64_t width, int max_
 extern "C" int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width, const int16_t* mask,
                                   int64_t mask_stride, const int32_t* lengths, int64_t rows,
                                   const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
-                                  const int32_t* cu_seqlens_q,
-                                  int64_t n_req, int max_splits, int n_cu, void* workspace, size_t workspace_bytes,
-                                  int32_t* out, hipStream_t stream) {
+                                  const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                                  void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream) {
   return topk_common(score, score_stride, width, mask, mask_stride, lengths, rows, page_table, pt_stride, pt_cols,
                      cu_seqlens_q, n_req, max_splits, n_cu, nullptr, workspace, workspace_bytes, out, stream,
                      "dsa_topk_transform");
@@ -783,9 +856,9 @@ extern "C" int dsa_topk_transform(const float* score, int64_t score_stride, int6
 extern "C" int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t width, const int16_t* mask,
                                       int64_t mask_stride, const int32_t* lengths, int64_t rows,
                                       const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
-                                      const int32_t* cu_seqlens_q,
-                                      int64_t n_req, int max_splits, int n_cu, const int32_t* hist_ws,
-                                      void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream) {
+                                      const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                                      int32_t* hist_ws, void* workspace, size_t workspace_bytes, int32_t* out,
+                                      hipStream_t stream) {
   DSA_REQUIRE(hist_ws != nullptr, "dsa_topk_transform_pre: hist_ws is null");
   return topk_common(score, score_stride, width, mask, mask_stride, lengths, rows, page_table, pt_stride, pt_cols,
                      cu_seqlens_q, n_req, max_splits, n_cu, hist_ws, workspace, workspace_bytes, out, stream,

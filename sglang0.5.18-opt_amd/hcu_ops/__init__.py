@@ -22,8 +22,9 @@ from . import _C
 _TOPK_IMPL = os.environ.get("HCU_TOPK_IMPL", "split")
 _TOPK_SPLITS = int(os.environ.get("HCU_TOPK_SPLITS", "8"))
 
-# HCU_MQA_PCTAS[_G1]: CTAs per request for grouped [single] rows; <= 0 uses the default split of
-# 8 pages (512 tokens) per CTA.  HCU_MQA_RPC: rows per CTA for groups (must divide the group).
+# HCU_MQA_PCTAS[_G1]: CTAs the K pages of grouped [single] rows are spread over (each CTA streams a
+# slice of one request); <= 0 uses twice the CU count.  HCU_MQA_RPC: rows sharing one K stream
+# for groups (must divide the group).
 # HCU_MQA_HIST_MAX_ROWS: build the top-k pass-1 histogram inside the logits kernel up to this
 # many rows (the top-k then skips its own pass 1).
 _MQA_PCTAS = int(os.environ.get("HCU_MQA_PCTAS", "0"))
@@ -31,20 +32,7 @@ _MQA_PCTAS_G1 = int(os.environ.get("HCU_MQA_PCTAS_G1", str(_MQA_PCTAS)))
 _MQA_RPC = int(os.environ.get("HCU_MQA_RPC", "2"))
 _MQA_HIST_MAX_ROWS = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS", "256"))
 _MQA_HIST = None  # (logits, hist_lens, zws) of the last mqa_logits with a fused histogram
-_N_CU = None
 _HEADS = (32, 64)
-
-
-def _n_cu():
-    global _N_CU
-    if _N_CU is None:
-        _N_CU = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
-    return _N_CU
-
-
-def _topk_splits(rows, width):
-    """Splits the split top-k uses for [rows, width] scores (>= 8192 tokens per slice)."""
-    return min(max((width + 8191) // 8192, 1), _n_cu() // max(rows, 1), min(_TOPK_SPLITS, 64))
 
 
 def sparse_mask_topk_transform(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk=2048):
@@ -102,8 +90,7 @@ def mqa_logits(q, kv_cache, weights, context_lens, block_table, max_context_len,
         rows_per_cta = 1 if group_size == 1 else _MQA_RPC
     use_hist = (hist_lens is not None and _TOPK_IMPL == "split" and rows <= _MQA_HIST_MAX_ROWS
                 and hist_lens.dtype == torch.int32 and hist_lens.dim() == 1
-                and hist_lens.shape[0] == rows and hist_lens.is_contiguous()
-                and _topk_splits(rows, max_context_len) > 1)
+                and hist_lens.shape[0] == rows and hist_lens.is_contiguous())
     logits, mask, zws = _C.mqa_logits_hist(q, kv_cache, weights, context_lens.view(-1), block_table,
                                            max_context_len, group_size, persistent_ctas, rows_per_cta,
                                            hist_lens if use_hist else None)
