@@ -20,7 +20,7 @@
 //    (P = total pages, T = the target CTA count), so each CTA streams ~P / T consecutive pages of
 //    a single group whatever the length mix; the grid (T + groups) depends only on shapes, so
 //    the launch can be captured in a hipGraph.  The CTA's block-table slice is staged in LDS; its
-//    4 waves take pages w, w+4, ... and prefetch the next page while computing the current one.
+//    4 waves take pages w, w+4, ... and keep the next two pages in flight while computing one.
 //  * Mask words of pages past a group's length are zeroed by CTA g (grid >= groups), so no
 //    separate mask memset is launched.
 //  * kHist: also the top-k pass-1 histogram (12-bit key[31:20] of the nonzero logits of rows
@@ -239,13 +239,16 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 
   int i = wave;
   if (i < n_local) {
-    PageRegs cur;
+    // Two pages in flight ahead of the one being computed; past the end the last page is
+    // loaded again (branch-free).
+    const int last = n_local - 1;
+    PageRegs cur, nx1;
     load_page(a.kv, a.page_stride, s_bt[i], lane, cur);
+    load_page(a.kv, a.page_stride, s_bt[min(i + kWavesPerCta, last)], lane, nx1);
     while (true) {
       const int in = i + kWavesPerCta;
-      PageRegs nxt;
-      // Branch-free prefetch: past the end the current page is loaded again.
-      load_page(a.kv, a.page_stride, s_bt[in < n_local ? in : i], lane, nxt);
+      PageRegs nx2;
+      load_page(a.kv, a.page_stride, s_bt[min(in + kWavesPerCta, last)], lane, nx2);
 
       float val[R];
 #pragma unroll
@@ -292,7 +295,8 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 
       i = in;
       if (i >= n_local) break;
-      cur = nxt;
+      cur = nx1;
+      nx1 = nx2;
     }
   }
 
@@ -404,10 +408,13 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   const int64_t n_groups = batch / rows_per_cta;
   DSA_REQUIRE(n_groups <= 0x3FFFFFFF, "dsa_mqa_logits_decode: batch too large");
   if (target_ctas <= 0) {
+    // Two CTAs fit a CU; the per-group rounding adds up to one CTA per group, so aim below the
+    // resident count by the group count to finish in one round of CTAs.
     int n_cu = 0;
     const int st = dsa_device_cu_count(&n_cu);
     if (st != DSA_OK) return st;
-    target_ctas = 2 * n_cu;
+    const int64_t slots = 2 * static_cast<int64_t>(n_cu);
+    target_ctas = static_cast<int>(slots - n_groups > n_cu ? slots - n_groups : n_cu);
   }
   // Keep every CTA's page slice within the LDS block-table stage: P / T <= kMaxCtaPages.
   const int64_t max_pages = n_groups * bt_pages;

@@ -247,54 +247,58 @@ struct Stage {
   int cap_c;
 };
 
-// Unordered collection over [begin, end): A = keys above bin t1 (fast path: positive keys),
-// C = keys in bin t1 (none on the fast path).  Wave-aggregated LDS atomics give positions.
+// One batch of kUnroll float4 groups per lane: loads first, use later.
+struct Batch {
+  uint32_t k[kUnroll][4];
+  uint32_t v[kUnroll];
+};
+
 template <bool kVec, int NT>
-__device__ void collect(const RowSrc& r, int begin, int end, const Meta& m, const Stage& st) {
-  RowSrc rr = r;
-  rr.len = end;
-  for (int b = begin + static_cast<int>(threadIdx.x) * 4; b < end; b += NT * 4 * kUnroll) {
-    uint32_t k[kUnroll][4];
-    uint32_t v[kUnroll];
+__device__ __forceinline__ void load_batch(const RowSrc& rr, int b, Batch& x) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = load_keys4<kVec>(rr, b + u * NT * 4, k[u]);
+  for (int u = 0; u < kUnroll; ++u) x.v[u] = load_keys4<kVec>(rr, b + u * NT * 4, x.k[u]);
+}
+
+// A = keys above bin t1 (fast path: positive keys), C = keys in bin t1 (none on the fast
+// path); wave-aggregated LDS atomics give the staging positions.
+template <int NT>
+__device__ __forceinline__ void process_batch(int b, const Batch& x, const Meta& m, const Stage& st) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int na = 0, nc = 0;
-      bool fa[4], fc[4];
+  for (int u = 0; u < kUnroll; ++u) {
+    int na = 0, nc = 0;
+    bool fa[4], fc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool valid = (x.v[u] >> j) & 1u;
+      const uint32_t d = x.k[u][j] >> 20;
+      fa[j] = valid && (m.fast ? x.k[u][j] > kZeroKey : d > m.t1);
+      fc[j] = valid && !m.fast && d == m.t1;
+      na += fa[j];
+      nc += fc[j];
+    }
+    int ta, tc;
+    int pa = wave_prefix_small(na, ta);
+    int pc = wave_prefix_small(nc, tc);
+    if (ta | tc) {  // wave-uniform
+      int base_a = 0, base_c = 0;
+      if (lane_id() == 0) {
+        if (ta) base_a = atomicAdd(st.n_a, ta);
+        if (tc) base_c = atomicAdd(st.n_c, tc);
+      }
+      base_a = __shfl(base_a, 0);
+      base_c = __shfl(base_c, 0);
+      const int i0 = b + u * NT * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const bool valid = (v[u] >> j) & 1u;
-        const uint32_t d = k[u][j] >> 20;
-        fa[j] = valid && (m.fast ? k[u][j] > kZeroKey : d > m.t1);
-        fc[j] = valid && !m.fast && d == m.t1;
-        na += fa[j];
-        nc += fc[j];
-      }
-      int ta, tc;
-      int pa = wave_prefix_small(na, ta);
-      int pc = wave_prefix_small(nc, tc);
-      if (ta | tc) {  // wave-uniform
-        int base_a = 0, base_c = 0;
-        if (lane_id() == 0) {
-          if (ta) base_a = atomicAdd(st.n_a, ta);
-          if (tc) base_c = atomicAdd(st.n_c, tc);
+        if (fa[j]) {
+          const int idx = base_a + pa++;
+          if (idx < st.cap_a) st.a[idx] = i0 + j;
         }
-        base_a = __shfl(base_a, 0);
-        base_c = __shfl(base_c, 0);
-        const int i0 = b + u * NT * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (fa[j]) {
-            const int idx = base_a + pa++;
-            if (idx < st.cap_a) st.a[idx] = i0 + j;
-          }
-          if (fc[j]) {
-            const int idx = base_c + pc++;
-            if (idx < st.cap_c) {
-              st.ck[idx] = k[u][j];
-              st.ci[idx] = i0 + j;
-            }
+        if (fc[j]) {
+          const int idx = base_c + pc++;
+          if (idx < st.cap_c) {
+            st.ck[idx] = x.k[u][j];
+            st.ci[idx] = i0 + j;
           }
         }
       }
@@ -302,20 +306,46 @@ __device__ void collect(const RowSrc& r, int begin, int end, const Meta& m, cons
   }
 }
 
+// Unordered collection over [begin, end) (lane offsets added here).  `first`, if given, holds
+// the already-loaded first batch (issued before the threshold was known, to overlap its latency).
+template <bool kVec, int NT>
+__device__ void collect(const RowSrc& r, int begin, int end, const Meta& m, const Stage& st, const Batch* first) {
+  RowSrc rr = r;
+  rr.len = end;
+  int b = begin + static_cast<int>(threadIdx.x) * 4;
+  if (first != nullptr) {
+    process_batch<NT>(b, *first, m, st);
+    b += NT * 4 * kUnroll;
+  }
+  for (; b < end; b += NT * 4 * kUnroll) {
+    Batch x;
+    load_batch<kVec, NT>(rr, b, x);
+    process_batch<NT>(b, x, m, st);
+  }
+}
+
 // Radix select over LDS members: the key `thr` such that `need` members have key >= thr and the
 // number of members with key > thr (returned in above).  key_of(e) / member(e) index 0..n-1.
+// d1_known >= 0: every member's key[31:20] is d1_known (the first digit pass is skipped).
 template <int NT, typename KeyOf, typename Member>
 __device__ uint32_t radix_select(int n, int need, KeyOf key_of, Member member, int* hist, int* s_wtot, int* s_res,
-                                 int& above) {
-  zero_lds<NT>(hist, kBins);
-  __syncthreads();
-  for (int e = threadIdx.x; e < n; e += NT)
-    if (member(e)) atomicAdd(&hist[key_of(e) >> 20], 1);
-  __syncthreads();
-  find_threshold<kBins, NT>(hist, need, s_wtot, s_res);
-  const uint32_t d1 = static_cast<uint32_t>(s_res[0]);
-  int ab = s_res[1];
-  const int need2 = need - s_res[1];
+                                 int& above, int d1_known = -1) {
+  uint32_t d1;
+  int ab = 0;
+  int need2 = need;
+  if (d1_known >= 0) {
+    d1 = static_cast<uint32_t>(d1_known);
+  } else {
+    zero_lds<NT>(hist, kBins);
+    __syncthreads();
+    for (int e = threadIdx.x; e < n; e += NT)
+      if (member(e)) atomicAdd(&hist[key_of(e) >> 20], 1);
+    __syncthreads();
+    find_threshold<kBins, NT>(hist, need, s_wtot, s_res);
+    d1 = static_cast<uint32_t>(s_res[0]);
+    ab = s_res[1];
+    need2 = need - s_res[1];
+  }
   zero_lds<NT>(hist, kBins);
   __syncthreads();
   for (int e = threadIdx.x; e < n; e += NT) {
@@ -354,11 +384,12 @@ struct ResolveLds {
 
 // Resolves the LDS candidates (all in bin t1, unordered) of a row whose above1 tokens above
 // bin t1 are already in dst[0, above1).
-__device__ void resolve_lds(ResolveLds& L, int n_c, int above1, const PtRow& pt, int32_t* dst) {
+__device__ void resolve_lds(ResolveLds& L, int n_c, uint32_t t1, int above1, const PtRow& pt, int32_t* dst) {
   const int need1 = kTopK - above1;
   int gt;
   const uint32_t thr = radix_select<kTk>(
-      n_c, need1, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt);
+      n_c, need1, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt,
+      static_cast<int>(t1));
   const int remaining = need1 - gt;
   const int tie_base = kTopK - remaining;
   // ties at thr: all of them, unless there are more than `remaining` -- then the lowest tokens,
@@ -533,7 +564,9 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   }
   const RowSrc r = row_src(a, row, len);
   int pos, zeros;
+  Batch first;
   if constexpr (kPre) {
+    load_batch<kVec, kTk>(r, static_cast<int>(threadIdx.x) * 4, first);  // overlaps the pass-1 loads
     const int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
     for (int i = threadIdx.x; i < kBins; i += kTk) L.hist[i] = gh[i];
     pos = a.gcnt[2 * row];
@@ -550,7 +583,7 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
   __syncthreads();
   Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
-  collect<kVec, kTk>(r, 0, len, m, st);
+  collect<kVec, kTk>(r, 0, len, m, st, kPre ? &first : nullptr);
   __syncthreads();
   const int n_a = min(L.misc[0], kTopK);
   const int n_c = L.misc[1];
@@ -559,7 +592,7 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
     ordered_scan<kVec>(
         r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
   } else if (n_c <= kCapC) {
-    resolve_lds(L, n_c, m.above1, pt, dst);
+    resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
   } else {
     resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
   }
@@ -629,6 +662,9 @@ __global__ __launch_bounds__(kTs) void topk_split_collect_kernel(const TopkArgs 
   const int begin = s * sl;
   if (begin >= len) return;
   const int end = min(begin + sl, len);
+  RowSrc r = row_src(a, row, end);
+  Batch first;
+  load_batch<kVec, kTs>(r, begin + static_cast<int>(threadIdx.x) * 4, first);  // overlaps the pass-1 loads
   const int pos = a.gcnt[2 * row];
   const int zeros = a.gcnt[2 * row + 1];
   const bool fast = pos <= kTopK && pos + zeros >= kTopK;
@@ -640,7 +676,7 @@ __global__ __launch_bounds__(kTs) void topk_split_collect_kernel(const TopkArgs 
   __syncthreads();
   const Meta m = row_meta<kTs>(hist, pos, zeros, s_wtot, s_res);
   Stage st{s_a, s_ck, s_ci, &s_n[0], &s_n[1], kTopK, kCapSlice};
-  collect<kVec, kTs>(row_src(a, row, len), begin, end, m, st);
+  collect<kVec, kTs>(r, begin, end, m, st, &first);
   __syncthreads();
   const int n_a = min(s_n[0], kTopK);
   const int n_c = s_n[1];
@@ -716,7 +752,7 @@ __global__ __launch_bounds__(kTk) void topk_split_finish_kernel(const TopkArgs a
     }
   }
   __syncthreads();
-  resolve_lds(L, n_c, m.above1, pt, dst);
+  resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
 }
 
 int split_count(int64_t rows, int64_t width, int max_splits, int n_cu) {

@@ -64,11 +64,12 @@ def test_decode_logits_sparse_and_negative_modes(gpu):
     products give exact zeros (mask bit clear), all-negative weights give negative logits."""
     case = wl.decode_case(9, [3000, 2500], group=1, heads=64)
     kvf = case.kv.view(case.kv.shape[0], -1).clone()
-    codes = kvf[:, :8192].view(-1, 128)
+    codes = kvf[:, :8192].contiguous().view(-1, 128)
     vals = codes.view(torch.float8_e4m3fn).float().abs()
     g = torch.Generator().manual_seed(1)
     pos = torch.rand(codes.shape[0], 1, generator=g) < 0.05
-    codes.copy_(torch.where(pos, vals, -vals).to(torch.float8_e4m3fn).view(torch.uint8))
+    signed = torch.where(pos, vals, -vals).to(torch.float8_e4m3fn).view(torch.uint8)
+    kvf[:, :8192] = signed.view(kvf.shape[0], 8192)
     case.kv = kvf.view(case.kv.shape)
     case.q = case.q.abs()
     case.w = case.w.abs()
