@@ -101,6 +101,19 @@ __device__ __forceinline__ int wave_prefix_small(int c, int& total) {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// x + x[lane ^ 16] and then + x[lane ^ 32], in every lane, with the gfx950 row-swap VALU ops
+// (v_permlane16_swap / v_permlane32_swap) instead of LDS-routed shuffles.  Swapping a register
+// with itself leaves lane l of the two results holding x[l] and x[l ^ 16] (resp. ^ 32), in an
+// order that makes the sum identical in all lanes of a pair.
+__device__ __forceinline__ float sum_lanes_16_32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 }  // namespace dsa
 
 // ------------------------------------------------------------------------------------------

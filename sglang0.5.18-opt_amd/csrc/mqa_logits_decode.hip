@@ -13,14 +13,14 @@
 //    straight from HBM with the same byte mapping (2 x 16 B per lane, 2 KB contiguous per wave),
 //    so the instruction's K ordering is the same permutation on both sides and cancels.
 //  * Result lane l holds heads 4*(l/16)+i of token l%16: the epilogue is an in-lane
-//    max/fma chain over H/4 values, two xor-shuffles (16, 32), and a lane select that leaves
+//    max/fma chain over H/4 values, a row-swap sum over lanes l^16 and l^32, and a lane select that leaves
 //    lane l with token l of the page.  One 256 B logits store and one K-scale load per page.
 //  * Balanced static grid: a row group is R rows of one request (one K page stream feeds all R
 //    rows).  Every CTA reads the groups' lengths and gives group g ceil(pages_g * T / P) CTAs
 //    (P = total pages, T = the target CTA count), so each CTA streams ~P / T consecutive pages of
 //    a single group whatever the length mix; the grid (T + groups) depends only on shapes, so
 //    the launch can be captured in a hipGraph.  The CTA's block-table slice is staged in LDS; its
-//    4 waves take pages w, w+4, ... and keep the next two pages in flight while computing one.
+//    4 waves take pages w, w+4, ... and keep the next two pages in flight while scoring one.
 //  * Mask words of pages past a group's length are zeroed by CTA g (grid >= groups), so no
 //    separate mask memset is launched.
 //  * kHist: also the top-k pass-1 histogram (12-bit key[31:20] of the nonzero logits of rows
@@ -53,12 +53,6 @@ __device__ __forceinline__ i32x8 load_frag(const uint8_t* p) {
   return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
 }
 
-__device__ __forceinline__ i32x8 load_frag_nt(const uint8_t* p) {
-  const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 16));
-  return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
-}
-
 struct PageRegs {
   i32x8 k[4];  // 4 sub-tiles of 16 tokens
   float scale; // scale of token lane_id() of the page
@@ -69,8 +63,8 @@ __device__ __forceinline__ void load_page(const uint8_t* __restrict__ kv, int64_
   const uint8_t* page = kv + static_cast<int64_t>(phys) * page_stride;
   const uint8_t* p = page + (lane & 15) * kHeadDim + (lane >> 4) * 32;
 #pragma unroll
-  for (int st = 0; st < 4; ++st) pr.k[st] = load_frag_nt(p + st * 16 * kHeadDim);
-  pr.scale = __builtin_nontemporal_load(reinterpret_cast<const float*>(page + kPageFp8Bytes) + lane);
+  for (int st = 0; st < 4; ++st) pr.k[st] = load_frag(p + st * 16 * kHeadDim);
+  pr.scale = reinterpret_cast<const float*>(page + kPageFp8Bytes)[lane];
 }
 
 struct DecodeArgs {
@@ -237,66 +231,72 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 #pragma unroll
   for (int r = 0; r < R; ++r) nz[r] = pos[r] = 0;
 
-  int i = wave;
-  if (i < n_local) {
-    // Two pages in flight ahead of the one being computed; past the end the last page is
-    // loaded again (branch-free).
-    const int last = n_local - 1;
-    PageRegs cur, nx1;
-    load_page(a.kv, a.page_stride, s_bt[i], lane, cur);
-    load_page(a.kv, a.page_stride, s_bt[min(i + kWavesPerCta, last)], lane, nx1);
-    while (true) {
-      const int in = i + kWavesPerCta;
-      PageRegs nx2;
-      load_page(a.kv, a.page_stride, s_bt[min(in + kWavesPerCta, last)], lane, nx2);
-
-      float val[R];
+  // Scores one page held in registers: MFMA tiles, weighted ReLU head sum, mask / logits stores
+  // and the fused pass-1 histogram.
+  auto score_page = [&](int i, const PageRegs& cur) {
+    float val[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) val[r] = 0.0f;
+    for (int r = 0; r < R; ++r) val[r] = 0.0f;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          f32x4 acc[HT];
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma_fp8(qf[r][ht], cur.k[st], f32x4{0.f, 0.f, 0.f, 0.f});
-          float s = 0.0f;
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s += fmaxf(acc[ht][e], 0.0f) * wf[r][ht * 4 + e];
-          }
-          s += __shfl_xor(s, 16);
-          s += __shfl_xor(s, 32);
-          val[r] = (lane >> 4) == st ? s : val[r];
-        }
-      }
-
-      const int p = p_begin + i;
-      const int token = p * kPage + lane;
+    for (int st = 0; st < 4; ++st) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float v = val[r] * cur.scale;
-        const bool live = token < len[r];
-        const bool keep = live && __float_as_uint(v) != 0u;
-        const uint64_t bits = __ballot(keep);
-        const int64_t row = row0 + r;
-        if (lane < 4) a.mask[row * a.mask_stride + p * 4 + lane] = static_cast<int16_t>((bits >> (16 * lane)) & 0xFFFFu);
-        if (live) a.logits[row * a.logits_stride + token] = v;
-        if constexpr (kHist) {
-          if (keep && token < hlim[r]) {
-            const uint32_t key = float_key(v);
-            atomicAdd(&s_hist[r * kBins + static_cast<int>(key >> 20)], 1);
-            ++nz[r];
-            pos[r] += key > kZeroKey;
-          }
+        f32x4 acc[HT];
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma_fp8(qf[r][ht], cur.k[st], f32x4{0.f, 0.f, 0.f, 0.f});
+        float s = 0.0f;
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += fmaxf(acc[ht][e], 0.0f) * wf[r][ht * 4 + e];
+        }
+        s = sum_lanes_16_32(s);
+        val[r] = (lane >> 4) == st ? s : val[r];
+      }
+    }
+    const int p = p_begin + i;
+    const int token = p * kPage + lane;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = val[r] * cur.scale;
+      const bool live = token < len[r];
+      const bool keep = live && __float_as_uint(v) != 0u;
+      const uint64_t bits = __ballot(keep);
+      const int64_t row = row0 + r;
+      if (lane < 4) a.mask[row * a.mask_stride + p * 4 + lane] = static_cast<int16_t>((bits >> (16 * lane)) & 0xFFFFu);
+      if (live) a.logits[row * a.logits_stride + token] = v;
+      if constexpr (kHist) {
+        if (keep && token < hlim[r]) {
+          const uint32_t key = float_key(v);
+          atomicAdd(&s_hist[r * kBins + static_cast<int>(key >> 20)], 1);
+          ++nz[r];
+          pos[r] += key > kZeroKey;
         }
       }
+    }
+  };
 
-      i = in;
+  // Pages w, w+4, ... with two pages in flight while one is scored.  The loop is unrolled over
+  // three register sets so that no set is copied (a copy would wait for its loads).
+  constexpr int kStepP = kWavesPerCta;
+  int i = wave;
+  if (i < n_local) {
+    PageRegs pa, pb, pc;
+    load_page(a.kv, a.page_stride, s_bt[i], lane, pa);
+    if (i + kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + kStepP], lane, pb);
+    while (true) {
+      if (i + 2 * kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + 2 * kStepP], lane, pc);
+      score_page(i, pa);
+      i += kStepP;
       if (i >= n_local) break;
-      cur = nx1;
-      nx1 = nx2;
+      if (i + 2 * kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + 2 * kStepP], lane, pa);
+      score_page(i, pb);
+      i += kStepP;
+      if (i >= n_local) break;
+      if (i + 2 * kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + 2 * kStepP], lane, pb);
+      score_page(i, pc);
+      i += kStepP;
+      if (i >= n_local) break;
     }
   }
 

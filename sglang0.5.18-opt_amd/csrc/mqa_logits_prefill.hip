@@ -10,7 +10,7 @@
 //    double-buffered LDS tile; rows are padded to 144 B so the 16 lanes reading 16 different
 //    keys at one byte offset fall into different banks;
 //  * per page and row: 4 key sub-tiles x H/16 MFMAs (v_mfma_f32_16x16x128_f8f6f4), then the
-//    epilogue of the decode kernel (max/fma over the lane's heads, xor-shuffles 16 and 32, lane
+//    epilogue of the decode kernel (max/fma over the lane's heads, row-swap sums over l^16, l^32, lane
 //    select) leaves lane l with key l of the page: one 256 B store per page and row;
 //  * causal skipping: a wave skips a page for a row once the page starts at or past len[row];
 //    the CTA stops after the last page any of its rows needs.
@@ -158,8 +158,7 @@ __global__ __launch_bounds__(kThreads, 2) void mqa_logits_prefill_kernel(const P
 #pragma unroll
             for (int i = 0; i < 4; ++i) s += fmaxf(acc[ht][i], 0.0f) * wf[r][ht * 4 + i];
           }
-          s += __shfl_xor(s, 16);
-          s += __shfl_xor(s, 32);
+          s = sum_lanes_16_32(s);
           val[r] = (lane >> 4) == st ? s : val[r];
         }
       }

@@ -31,7 +31,7 @@ def check_logits(got, ref, mag, what=""):
     bad = err > RTOL * mag + 1e-30
     worst_mag = float((err / np.maximum(mag, 1e-30)).max()) if err.size else 0.0
     assert not bad.any(), f"{what}: {int(bad.sum())} logits outside {RTOL} * magnitude; worst {worst_mag:.3e}"
-    plain = np.abs(ref) >= mag / CANCEL
+    plain = (np.abs(ref) >= mag / CANCEL) & (mag > 0)  # exact zeros are covered by (a)
     rel = err[plain] / np.abs(ref[plain]) if plain.any() else np.zeros(1)
     worst_rel = float(rel.max())
     assert worst_rel <= RTOL, f"{what}: relative error {worst_rel:.3e} > {RTOL} on an uncancelled logit"
