@@ -22,9 +22,11 @@ ARCH = "gfx950"
 
 HIP_SOURCES = ["status.cpp", "dequant.hip", "quant.hip", "mqa_logits_decode.hip", "mqa_logits_prefill.hip",
                "topk.hip"]
-# Packed fp32 VALU ops (v_pk_fma_f32 and friends) are switched off for every HIP source.
+# Packed fp32 VALU ops (v_pk_fma_f32 and friends) are switched off for every HIP source.  MFMA
+# results are written to VGPRs directly (the epilogues read them with VALU ops; the AGPR form
+# would add one v_accvgpr_read per result element).
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-             "-packed-fp32-ops", "-Wall", "-Wno-unused-command-line-argument"]
+             "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1", "-Wall", "-Wno-unused-command-line-argument"]
 
 
 def _run(cmd):

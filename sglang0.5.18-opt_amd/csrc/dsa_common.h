@@ -101,6 +101,11 @@ __device__ __forceinline__ int wave_prefix_small(int c, int& total) {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// max(x, +0) as one integer max on the float bits: negative floats (and -0.0) are negative
+// integers, so they become +0; other values, NaNs included, pass unchanged.  fmaxf would add a
+// NaN-quieting max per element.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
 // x + x[lane ^ 16] and then + x[lane ^ 32], in every lane, with the gfx950 row-swap VALU ops
 // (v_permlane16_swap / v_permlane32_swap) instead of LDS-routed shuffles.  Swapping a register
 // with itself leaves lane l of the two results holding x[l] and x[l ^ 16] (resp. ^ 32), in an

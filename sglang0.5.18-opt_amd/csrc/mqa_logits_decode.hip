@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s += fmaxf(acc[ht][e], 0.0f) * wf[r][ht * 4 + e];
+          for (int e = 0; e < 4; ++e) s += relu_bits(acc[ht][e]) * wf[r][ht * 4 + e];
         }
         s = sum_lanes_16_32(s);
         val[r] = (lane >> 4) == st ? s : val[r];
@@ -277,23 +277,27 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
   };
 
   // Pages w, w+4, ... with two pages in flight while one is scored.  The loop is unrolled over
-  // three register sets so that no set is copied (a copy would wait for its loads).
+  // three register sets so that no set is copied (a copy would wait for its loads), and the
+  // prefetches are unconditional -- past the end they re-read the wave's last page, an L2 hit --
+  // so the in-order load counter only ever waits for the page being scored.
   constexpr int kStepP = kWavesPerCta;
   int i = wave;
   if (i < n_local) {
+    const int last = wave + (n_local - 1 - wave) / kStepP * kStepP;
+    auto page_of = [&](int k) { return s_bt[k < last ? k : last]; };
     PageRegs pa, pb, pc;
-    load_page(a.kv, a.page_stride, s_bt[i], lane, pa);
-    if (i + kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + kStepP], lane, pb);
+    load_page(a.kv, a.page_stride, page_of(i), lane, pa);
+    load_page(a.kv, a.page_stride, page_of(i + kStepP), lane, pb);
     while (true) {
-      if (i + 2 * kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + 2 * kStepP], lane, pc);
+      load_page(a.kv, a.page_stride, page_of(i + 2 * kStepP), lane, pc);
       score_page(i, pa);
       i += kStepP;
       if (i >= n_local) break;
-      if (i + 2 * kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + 2 * kStepP], lane, pa);
+      load_page(a.kv, a.page_stride, page_of(i + 2 * kStepP), lane, pa);
       score_page(i, pb);
       i += kStepP;
       if (i >= n_local) break;
-      if (i + 2 * kStepP < n_local) load_page(a.kv, a.page_stride, s_bt[i + 2 * kStepP], lane, pb);
+      load_page(a.kv, a.page_stride, page_of(i + 2 * kStepP), lane, pb);
       score_page(i, pc);
       i += kStepP;
       if (i >= n_local) break;

@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kThreads, 2) void mqa_logits_prefill_kernel(const P
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s += fmaxf(acc[ht][i], 0.0f) * wf[r][ht * 4 + i];
+            for (int i = 0; i < 4; ++i) s += relu_bits(acc[ht][i]) * wf[r][ht * 4 + i];
           }
           s = sum_lanes_16_32(s);
           val[r] = (lane >> 4) == st ? s : val[r];
