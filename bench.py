@@ -46,6 +46,20 @@ WORKLOADS = {
 }
 
 
+def profiled_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from its committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the counter's reading for a copy of known size),
+    or None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}.{workload}.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -284,6 +298,9 @@ def main(argv=None):
     ap.add_argument("--workload", default="decode_mtp64", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB three times (the known-size kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs the indexer on one GPU only: this build has no multi-GPU path "
@@ -294,6 +311,15 @@ def main(argv=None):
     from hcu_ops import workloads as wl
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 18
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes n * 4 bytes
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 copies of {args.copy_calibration_mib} MiB")
+        del src, dst
     t0 = time.perf_counter()
     case = getattr(wl, args.workload)()
     log(f"built {args.workload} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
@@ -319,25 +345,29 @@ def main(argv=None):
     value = tokens / 1e3 / (ms / 1e3)
     log(f"timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
 
-    k_ms = kernel_time_ms(step.logits_only, torch)
     if decode:
-        kh_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
+        # the launch as the step makes it: logits + fused top-k pass 1 (+ its workspace seeding)
+        k_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
+        k0_ms = kernel_time_ms(step.logits_only, torch)
         kb = step.logits_bytes()
         achieved = kb / (k_ms / 1e3) / 1e9
+        traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", args.workload)
         roofline = {"bound": "hbm", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": None, "algorithmic_bytes": kb, "kernel_us": round(k_ms * 1e3, 2),
-                    "with_fused_pass1_us": round(kh_ms * 1e3, 2)}
+                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_bytes": kb,
+                    "kernel_us": round(k_ms * 1e3, 2), "without_fused_pass1_us": round(k0_ms * 1e3, 2)}
         pb = step.path_bytes()
         pa = pb / (ms / 1e3) / 1e9
         path = {"bound": "hbm", "achieved": round(pa, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(pa / HBM_PEAK_GBS, 4), "algorithmic_bytes": pb}
     else:
+        k_ms = kernel_time_ms(step.logits_only, torch)
         kf = step.logits_flops()
         achieved = kf / (k_ms / 1e3) / 1e12
+        traffic, tsrc = profiled_traffic("mqa_logits_prefill_kernel", args.workload)
         roofline = {"bound": "mfma", "kernel": "mqa_logits_prefill_kernel", "achieved": round(achieved, 1),
                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                    "traffic": None, "algorithmic_flops": kf, "kernel_us": round(k_ms * 1e3, 2)}
+                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_flops": kf, "kernel_us": round(k_ms * 1e3, 2)}
         pf = step.path_flops()
         pa = pf / (ms / 1e3) / 1e12
         path = {"bound": "mfma", "achieved": round(pa, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
