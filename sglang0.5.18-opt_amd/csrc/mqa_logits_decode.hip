@@ -340,7 +340,8 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
 // Seeds the top-k pass-1 workspace: every token below min(hist_len, width) counts as a zero
 // until the logits kernel subtracts its nonzero ones.  Rows with <= 2048 tokens stay empty.
 // Of the second histogram block of the layout ([ghist1 | ghist2 | cnt], the reference's
-// workspace size) only word 0 of each row is used -- as the top-k's output counter -- and zeroed.
+// workspace size) only words 0..2 of each row are used -- as the split top-k's per-row counters
+// -- and zeroed.
 __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __restrict__ hist_lens, int width,
                                                             int64_t batch, int32_t* __restrict__ ws) {
   const int64_t row = blockIdx.x;
@@ -353,8 +354,8 @@ __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __res
     int32_t* c = ws + 2 * batch * kBins + 2 * row;
     c[0] = 0;
     c[1] = zeros;
-    ws[(batch + row) * kBins] = 0;
   }
+  if (threadIdx.x < 3) ws[(batch + row) * kBins + threadIdx.x] = 0;
 }
 
 template <int H, int R, bool kHist>
