@@ -99,19 +99,21 @@ int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* s
  * mask [B, width / 16] i16 with row stride mask_stride: every word is written.
  * heads in {32, 64}; B % group_size == 0; rows_per_cta divides group_size and is in {1,2,3,4}.
  * target_ctas: number of CTAs the K pages are spread over, each CTA streaming a slice of one
- * request (<= 0: twice the CU count); the grid is target_ctas + B / rows_per_cta.
- * hist_lens (nullable, int32 [B]) with hist_ws (int32 [B * (2 * 4096 + 2)]): also build pass 1
- * of the top-k (12-bit key histogram + positive / zero counts of every row whose
- * min(hist_lens[r], width) > 2048) into hist_ws, in the layout dsa_topk_transform_pre consumes:
- * [12-bit histograms rows*4096 | second block rows*4096 | (positives, zeros) rows*2]; of the
- * second block only word 0 of each row is written (zero, the top-k's output counter). */
+ * request (<= 0: as many as are resident at once); the grid is target_ctas + B / rows_per_cta.
+ * hist_ws (nullable, int32 [B * (2 * 4096 + 2)], 16-B aligned): the pass-1 workspace of a
+ * following dsa_topk_transform_pre, in its layout [12-bit histograms rows*4096 | second block
+ * rows*4096 | (positives, zeros) rows*2]; of the second block only words 0..2 of each row are
+ * used (the split top-k's per-row counters).  fuse_pass1 = 0: hist_ws is zeroed (the top-k
+ * builds pass 1); fuse_pass1 = 1 (needs hist_lens, int32 [B], and rows_per_cta <= 3): pass 1
+ * (12-bit key histogram + positive / zero counts of every row whose min(hist_lens[r], width) >
+ * 2048) is built here, inside the logits kernel (reference: the fused kHist path). */
 int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t batch,
                           int group_size, const uint8_t* kv_cache, int64_t page_stride_bytes,
                           const int32_t* context_lens, const int32_t* block_table,
                           int64_t bt_stride, int64_t bt_pages, float* logits,
                           int64_t logits_stride, int16_t* mask, int64_t mask_stride,
                           int rows_per_cta, int target_ctas, const int32_t* hist_lens,
-                          int32_t* hist_ws, hipStream_t stream);
+                          int32_t* hist_ws, int fuse_pass1, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Prefill MQA indexer logits (the role of the prefill indexer's fp8 logits kernel, sglang
@@ -156,13 +158,14 @@ int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
 /* dsa_topk_transform with pass 1 (histogram and counts) already built into hist_ws by
  * dsa_mqa_logits_decode(hist_lens = lengths) (replaces
  * _C.sparse_mask_topk_transform_split_pre, sparse_mask_topk.cu:986-1051).  hist_ws is the
- * int32 [rows * (2 * 4096 + 2)] buffer given to the logits call (its per-row output counter is
- * updated, so a hist_ws serves one top-k call); `workspace` as above. */
+ * int32 [rows * (2 * 4096 + 2)] buffer given to the logits call; pass1_done says whether that
+ * call built pass 1 (fuse_pass1), else pass 1 is built here into it (the logits call zeroed it).
+ * Its per-row counters are consumed, so a hist_ws serves one top-k call; `workspace` as above. */
 int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t width,
                            const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
                            int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
                            const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
-                           int32_t* hist_ws, void* workspace, size_t workspace_bytes,
+                           int32_t* hist_ws, int pass1_done, void* workspace, size_t workspace_bytes,
                            int32_t* out, hipStream_t stream);
 
 #ifdef __cplusplus

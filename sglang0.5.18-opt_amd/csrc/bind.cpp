@@ -41,12 +41,14 @@ void check_kv(const torch::Tensor& kv_cache) {
 
 // ------------------------------------------------------------------------------------------------
 // Logits (hcu_ops/csrc/mqa_hist.cu:324-405).  persistent_ctas > 0 sets the number of CTAs the
-// K pages are spread over (<= 0: twice the CU count); hist_lens builds top-k pass 1 into zws.
+// K pages are spread over (<= 0: every CTA resident at once).  hist_lens: also return zws, the
+// top-k's pass-1 workspace, zeroed (the paired top-k builds pass 1) or, with fuse_pass1, with
+// pass 1 built inside the logits kernel.
 std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::Tensor& kv_cache,
                                            const torch::Tensor& weights, const torch::Tensor& context_lens,
                                            const torch::Tensor& block_table, int64_t max_context_len,
                                            int64_t group_size, int64_t persistent_ctas, int64_t rows_per_cta,
-                                           const c10::optional<torch::Tensor>& hist_lens) {
+                                           const c10::optional<torch::Tensor>& hist_lens, bool fuse_pass1) {
   TORCH_CHECK(q.is_cuda() && q.scalar_type() == at::kFloat8_e4m3fn && q.dim() == 4 && q.size(1) == 1 &&
                   (q.size(2) == 32 || q.size(2) == 64) && q.size(3) == kHeadDim && q.is_contiguous(),
               "q must be contiguous fp8 e4m3fn [B, 1, H, 128] with H in {32, 64}");
@@ -83,7 +85,8 @@ std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::
       static_cast<int>(group_size), kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), context_lens.data_ptr<int>(),
       block_table.data_ptr<int>(), block_table.stride(0), pages, logits.data_ptr<float>(), logits.stride(0),
       mask.data_ptr<int16_t>(), mask_stride, static_cast<int>(rows_per_cta), target,
-      hist ? hist_lens->data_ptr<int>() : nullptr, hist ? zws.data_ptr<int>() : nullptr, cur_stream()));
+      hist ? hist_lens->data_ptr<int>() : nullptr, hist ? zws.data_ptr<int>() : nullptr, hist && fuse_pass1 ? 1 : 0,
+      cur_stream()));
   return {logits, mask, zws};
 }
 
@@ -112,7 +115,7 @@ void check_topk(const torch::Tensor& score, const c10::optional<torch::Tensor>& 
 torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::Tensor>& nonzero_mask,
                         const torch::Tensor& lengths, const torch::Tensor& page_table_size_1,
                         const torch::Tensor& cu_seqlens_q, int64_t topk, int64_t max_splits,
-                        const torch::Tensor* zws) {
+                        const torch::Tensor* zws, bool pass1_done) {
   check_topk(score, nonzero_mask, lengths, page_table_size_1, topk);
   const int64_t rows = score.size(0);
   const int64_t width = score.size(1);
@@ -142,7 +145,8 @@ torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::T
     st = dsa_topk_transform_pre(score.data_ptr<float>(), score.stride(0), width, mp, ms, lengths.data_ptr<int>(),
                                 rows, page_table_size_1.data_ptr<int>(), page_table_size_1.stride(0),
                                 page_table_size_1.size(1), cu, n_req,
-                                splits, cus, zws->data_ptr<int>(), ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
+                                splits, cus, zws->data_ptr<int>(), pass1_done ? 1 : 0,
+                                ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
                                 dst.data_ptr<int>(), cur_stream());
   } else {
     st = dsa_topk_transform(score.data_ptr<float>(), score.stride(0), width, mp, ms, lengths.data_ptr<int>(), rows,
@@ -157,28 +161,30 @@ torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::T
 torch::Tensor sparse_mask_topk_transform(const torch::Tensor& score, const torch::Tensor& nonzero_mask,
                                          const torch::Tensor& lengths, const torch::Tensor& page_table_size_1,
                                          const torch::Tensor& cu_seqlens_q, int64_t topk) {
-  return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, 1, nullptr);
+  return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, 1, nullptr, false);
 }
 
 torch::Tensor sparse_mask_topk_transform_split(const torch::Tensor& score, const torch::Tensor& nonzero_mask,
                                                const torch::Tensor& lengths, const torch::Tensor& page_table_size_1,
                                                const torch::Tensor& cu_seqlens_q, int64_t topk, int64_t max_splits) {
-  return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, nullptr);
+  return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, nullptr, false);
 }
 
 torch::Tensor sparse_mask_topk_transform_split_pre(const torch::Tensor& score, const torch::Tensor& nonzero_mask,
                                                    const torch::Tensor& lengths,
                                                    const torch::Tensor& page_table_size_1,
                                                    const torch::Tensor& cu_seqlens_q, int64_t topk,
-                                                   int64_t max_splits, const torch::Tensor& zws) {
-  return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, &zws);
+                                                   int64_t max_splits, const torch::Tensor& zws,
+                                                   bool pass1_done) {
+  return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, &zws,
+                   pass1_done);
 }
 
 // Dense-score top-k (no sparse mask: every score below the row length is valid), e.g. prefill.
 torch::Tensor topk_transform(const torch::Tensor& score, const torch::Tensor& lengths,
                              const torch::Tensor& page_table_size_1, const torch::Tensor& cu_seqlens_q,
                              int64_t topk, int64_t max_splits) {
-  return topk_impl(score, c10::nullopt, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, nullptr);
+  return topk_impl(score, c10::nullopt, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, nullptr, false);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -288,14 +294,20 @@ torch::Tensor mqa_logits_prefill(const torch::Tensor& q, const torch::Tensor& we
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mqa_logits_hist", &mqa_logits_hist,
-        "paged fp8 MQA indexer logits + 16-token nonzero mask -> {logits, mask, zws}; with hist_lens also "
-        "top-k pass 1 into zws");
+        "paged fp8 MQA indexer logits + 16-token nonzero mask -> {logits, mask, zws}; with hist_lens zws is the "
+        "paired top-k's pass-1 workspace (zeroed, or filled when fuse_pass1)",
+        py::arg("q"), py::arg("kv_cache"), py::arg("weights"), py::arg("context_lens"), py::arg("block_table"),
+        py::arg("max_context_len"), py::arg("group_size"), py::arg("persistent_ctas"), py::arg("rows_per_cta"),
+        py::arg("hist_lens"), py::arg("fuse_pass1") = false);
   m.def("sparse_mask_topk_transform", &sparse_mask_topk_transform,
         "Exact top-2048 + page-table transform over sparse-mask MQA logits (one CTA per row)");
   m.def("sparse_mask_topk_transform_split", &sparse_mask_topk_transform_split,
         "Same as sparse_mask_topk_transform; few rows are split over several CTAs");
   m.def("sparse_mask_topk_transform_split_pre", &sparse_mask_topk_transform_split_pre,
-        "sparse_mask_topk_transform_split with pass 1 taken from mqa_logits_hist's workspace");
+        "sparse_mask_topk_transform_split on mqa_logits_hist's pass-1 workspace (pass1_done: built there)",
+        py::arg("score"), py::arg("nonzero_mask"), py::arg("lengths"), py::arg("page_table_size_1"),
+        py::arg("cu_seqlens_q"), py::arg("topk"), py::arg("max_splits"), py::arg("zws"),
+        py::arg("pass1_done") = false);
   m.def("topk_transform", &topk_transform, "Exact top-2048 + page-table transform over dense scores");
   m.def("dequant_k_paged", &dequant_k_paged, "indexer 132-B paged fp8 K -> bf16 [n, 128]");
   m.def("gather_k_paged", &gather_k_paged, "indexer 132-B paged fp8 K -> contiguous (fp8 [n, 128], f32 [n])");

@@ -9,25 +9,33 @@
 //
 //  * One MFMA computes a [16 heads x 16 tokens] tile with the whole 128-deep contraction.  The
 //    A operand is q (heads), held in VGPRs for the life of the wave: lane l holds head
-//    tile*16 + l%16, bytes (l/16)*32 .. +32.  The B operand is 16 tokens of a K page loaded
-//    straight from HBM with the same byte mapping (2 x 16 B per lane, 2 KB contiguous per wave),
-//    so the instruction's K ordering is the same permutation on both sides and cancels.
+//    tile*16 + l%16, bytes (l/16)*32 .. +32.  The B operand is 16 tokens of a K page with the
+//    same byte mapping, so the instruction's K ordering is the same permutation on both sides
+//    and cancels.
 //  * Result lane l holds heads 4*(l/16)+i of token l%16: the epilogue is an in-lane
-//    max/fma chain over H/4 values, a row-swap sum over lanes l^16 and l^32, and a lane select that leaves
-//    lane l with token l of the page.  One 256 B logits store and one K-scale load per page.
-//  * Balanced static grid: a row group is R rows of one request (one K page stream feeds all R
-//    rows).  Every CTA reads the groups' lengths and gives group g ceil(pages_g * T / P) CTAs
-//    (P = total pages, T = the target CTA count), so each CTA streams ~P / T consecutive pages of
-//    a single group whatever the length mix; the grid (T + groups) depends only on shapes, so
-//    the launch can be captured in a hipGraph.  The CTA's block-table slice is staged in LDS; its
-//    4 waves take pages w, w+4, ... and keep the next two pages in flight while scoring one.
-//  * Mask words of pages past a group's length are zeroed by CTA g (grid >= groups), so no
-//    separate mask memset is launched.
+//    max/fma chain over H/4 values, a row-swap sum over lanes l^16 and l^32, and a lane select
+//    that leaves lane l with token l of the page.  One 256 B logits store per page and row.
+//  * K pages go HBM -> LDS by DMA (global_load_lds_dwordx4: no VGPR staging, so register
+//    pressure does not limit the loads in flight).  A CTA runs S page streams; a stream's R
+//    waves (one per row of the group) share each page through an LDS slot, and while a page is
+//    scored the stream's next page lands in the other slot.  The 16-B chunks of a token are
+//    XOR-swizzled in the slot so that the MFMA-layout ds_read_b128s are conflict-free.  A
+//    stream's waves meet at one bare s_barrier per page, after each waited for its own share
+//    of the DMA (explicit vmcnt); a page's stores are issued at the next step, before its DMA,
+//    so that wait never covers them.  S, the slot count and the CTA's block-table slice are
+//    chosen per (R, histogram) for LDS / register fit (Shape).
+//  * Balanced static grid: a row group is R rows of one request.  Every CTA reads the groups'
+//    lengths and gives group g ceil(pages_g * T / P) CTAs (P = total pages, T = the target CTA
+//    count), so each CTA streams ~P / T consecutive pages of a single group whatever the length
+//    mix; the grid (T + groups) depends only on shapes, so the launch can be captured in a
+//    hipGraph, and T is chosen so that every CTA is resident at once.
+//  * Mask words past a group's pages are zeroed by the group's own CTAs (a share each, 8-B
+//    stores), so no separate mask memset is launched; a group with no pages still gets a CTA.
 //  * kHist: also the top-k pass-1 histogram (12-bit key[31:20] of the nonzero logits of rows
-//    with min(hist_len, width) > 2048, plus positive / zero counts), as LDS counts flushed once
-//    per CTA with one global atomic per nonzero bin; mqa_hist_init_kernel seeds the zero bin /
-//    zero count with the row length (mqa_hist.cu:278-304) and every CTA subtracts its nonzero
-//    tokens.
+//    with min(hist_len, width) > 2048, plus positive / zero counts), as 16-bit LDS counts (two
+//    bins a word; a CTA's tokens per row stay below 2^16) flushed once per CTA with one global
+//    atomic per nonzero bin; mqa_hist_init_kernel seeds the zero bin / zero count with the row
+//    length (mqa_hist.cu:278-304) and every CTA subtracts its nonzero tokens.
 #include "dsa_common.h"
 
 namespace dsa {
@@ -37,9 +45,8 @@ using i32x8 = __attribute__((ext_vector_type(8))) int;
 using f32x4 = __attribute__((ext_vector_type(4))) float;
 using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 
-constexpr int kThreads = 256;
-constexpr int kWavesPerCta = kThreads / kWave;
-constexpr int kMaxCtaPages = 1024;  // host keeps P / T <= 1024 so the block-table slice fits LDS
+constexpr int kLdsBytes = 163840;  // LDS per CU
+constexpr int kMaxWavesCu = 16;    // waves per CU the register budget (<= 128 VGPRs) allows
 
 __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
   // scale operands 0 select the unscaled v_mfma_f32_16x16x128_f8f6f4 (both operands fp8 e4m3)
@@ -53,18 +60,32 @@ __device__ __forceinline__ i32x8 load_frag(const uint8_t* p) {
   return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
 }
 
-struct PageRegs {
-  i32x8 k[4];  // 4 sub-tiles of 16 tokens
-  float scale; // scale of token lane_id() of the page
-};
+// LDS chunk (16 B units) of token t's K bytes [16 p, 16 p + 16) within a page slot: rows of
+// 8 chunks, chunk p of token t stored at position p ^ ((t >> 1) & 7), so the 16 lanes of one
+// ds_read_b128 (16 consecutive tokens, the same p) hit 16 distinct 16-B bank groups.
+__device__ __forceinline__ int swz(int t, int p) { return t * 8 + (p ^ ((t >> 1) & 7)); }
 
-__device__ __forceinline__ void load_page(const uint8_t* __restrict__ kv, int64_t page_stride, int phys, int lane,
-                                          PageRegs& pr) {
-  const uint8_t* page = kv + static_cast<int64_t>(phys) * page_stride;
-  const uint8_t* p = page + (lane & 15) * kHeadDim + (lane >> 4) * 32;
+// DMA of one page (8448 B) into an LDS slot by the R waves of a stream, global -> LDS with no
+// register staging.  Block j (j = r, r + R, ...; 1 KB = tokens 8j .. 8j + 7): lane i fills slot
+// chunk 64 j + i with the global chunk that belongs there; the last wave also copies the 64
+// token scales behind the K bytes.
+template <int R>
+__device__ __forceinline__ void dma_page(const uint8_t* page, uint8_t* slot, int r, int lane) {
 #pragma unroll
-  for (int st = 0; st < 4; ++st) pr.k[st] = load_frag(p + st * 16 * kHeadDim);
-  pr.scale = reinterpret_cast<const float*>(page + kPageFp8Bytes)[lane];
+  for (int j = r; j < 8; j += R) {
+    const int c = j * 64 + lane;
+    const int t = c >> 3;
+    const int p = (c & 7) ^ ((t >> 1) & 7);
+    __builtin_amdgcn_global_load_lds(page + t * kHeadDim + p * 16, slot + j * 1024, 16, 0, 0);
+  }
+  if (r == R - 1) __builtin_amdgcn_global_load_lds(page + kPageFp8Bytes + lane * 4, slot + kPageFp8Bytes, 4, 0, 0);
+}
+
+// 32 bytes (chunks p0, p0 + 1) of token t from a slot, as an MFMA operand.
+__device__ __forceinline__ i32x8 lds_frag(const uint8_t* slot, int t, int p0) {
+  const u32x4 a = *reinterpret_cast<const u32x4*>(slot + swz(t, p0) * 16);
+  const u32x4 b = *reinterpret_cast<const u32x4*>(slot + swz(t, p0 + 1) * 16);
+  return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
 }
 
 struct DecodeArgs {
@@ -86,7 +107,8 @@ struct DecodeArgs {
   int n_groups;  // batch / R
   int target;    // T: CTAs the pages are spread over
   const int32_t* hist_lens;
-  int32_t* hist_ws;
+  int32_t* hist_ws;   // kHist: the fused pass-1 workspace
+  int32_t* zero_ws;   // non-null: a pass-1 workspace the top-k fills, zeroed here
   int64_t batch;
 };
 
@@ -99,12 +121,14 @@ __device__ __forceinline__ int group_pages(const DecodeArgs& a, int g) {
   return (m + kPage - 1) / kPage;
 }
 
+// A group with no pages still gets one CTA: it zeroes the group's mask rows.
 __device__ __forceinline__ int group_ctas(int pages, int total_pages, int target) {
-  if (pages == 0) return 0;
+  if (pages == 0) return 1;
   return static_cast<int>((static_cast<int64_t>(pages) * target + total_pages - 1) / total_pages);
 }
 
-// Block-wide (256 threads) sum and exclusive prefix.
+// Block-wide (NT threads) sum and exclusive prefix.
+template <int NT>
 __device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -118,7 +142,7 @@ __device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
   __syncthreads();
   int before = 0, tot = 0;
 #pragma unroll
-  for (int v = 0; v < kWavesPerCta; ++v) {
+  for (int v = 0; v < NT / kWave; ++v) {
     before += v < w ? s_w[v] : 0;
     tot += s_w[v];
   }
@@ -127,14 +151,64 @@ __device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
   return before + inc - x;
 }
 
+// Launch shape per (rows per CTA R, fused histogram): S page streams per CTA with NS LDS slots
+// each, and the block-table slice a CTA stages (the host keeps P / T within it; it also bounds a
+// row's tokens per CTA below 2^16 for the 16-bit histogram counters).  Measured on the 64-request
+// MTP decode: one stream per CTA (eight CTAs per CU) without the histogram; with it, the 8 KB
+// per row of counters is amortised over two streams (R = 2) or four (R = 1).
+template <int R, bool kHist>
+struct Shape {
+  static constexpr int S = kHist ? (R == 1 ? 4 : (R == 2 ? 2 : 1)) : 1;
+  static constexpr int NS = 2;
+  static constexpr int kMaxPages = S == 1 ? 255 : (S == 2 ? 511 : 1023);
+  static constexpr int kLds = S * NS * kPageBytes + (kHist ? R * kBins * 2 : 0) + kMaxPages * 4 + 512;
+  static constexpr int kByLds = kLdsBytes / kLds;
+  static constexpr int kByWaves = kMaxWavesCu / (R * S) > 0 ? kMaxWavesCu / (R * S) : 1;
+  static constexpr int kCtasPerCu = kByLds < kByWaves ? kByLds : kByWaves;
+  static constexpr int kThreads = R * S * kWave;
+  static constexpr int kWavesPerSimd = (kCtasPerCu * R * S + 3) / 4;
+};
+
+// VMEM ops of wave r's share of a page DMA (blocks r, r + R, ... of 8; the last wave adds the
+// scales).
+template <int R>
+__device__ __forceinline__ int dma_ops(int r) { return (8 - r + R - 1) / R + (r == R - 1 ? 1 : 0); }
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in 0..15 (gfx9 encoding; expcnt / lgkmcnt not waited).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+  }
+}
+
+
+
 template <int H, int R, bool kHist>
-__global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_waves_per_eu(
+    Shape<R, kHist>::kWavesPerSimd))) void mqa_logits_decode_kernel(const DecodeArgs a) {
   constexpr int HT = H / 16;  // head tiles
-  extern __shared__ int s_hist[];  // kHist: [R][kBins]
+  using Sh = Shape<R, kHist>;
+  constexpr int S = Sh::S;
+  constexpr int NS = Sh::NS;
+  static_assert(NS == 2 || NS == 3, "2 or 3 page slots per stream");
+  constexpr int NT = Sh::kThreads;
+  __shared__ __attribute__((aligned(16))) uint8_t s_slot0[S][kPageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_slot1[S][kPageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_slot2[NS > 2 ? S : 1][NS > 2 ? kPageBytes : 16];
+  __shared__ uint32_t s_hist[kHist ? R * kBins / 2 : 1];  // 16-bit counters, two bins per word
   __shared__ int s_cnt[2 * R];
-  __shared__ int s_w[kWavesPerCta];
+  __shared__ int s_w[NT / kWave];
   __shared__ int s_assign[3];  // group, index within the group's CTAs, the group's CTA count
-  __shared__ int s_bt[kMaxCtaPages];
+  __shared__ int s_bt[Sh::kMaxPages];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -142,18 +216,18 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
   const int cta = blockIdx.x;
 
   // ---- work assignment (identical in every CTA) ----
-  const int per_t = (a.n_groups + kThreads - 1) / kThreads;
+  const int per_t = (a.n_groups + NT - 1) / NT;
   const int g_lo = min(tid * per_t, a.n_groups);
   const int g_hi = min(g_lo + per_t, a.n_groups);
   int my_pages = 0;
   for (int g = g_lo; g < g_hi; ++g) my_pages += group_pages(a, g);
   int total_pages;
-  block_excl(my_pages, total_pages, s_w);
+  block_excl<NT>(my_pages, total_pages, s_w);
   if (tid == 0) s_assign[0] = -1;
   int my_ctas = 0;
   for (int g = g_lo; g < g_hi; ++g) my_ctas += group_ctas(group_pages(a, g), total_pages, a.target);
   int total_ctas;
-  int c0 = block_excl(my_ctas, total_ctas, s_w);
+  int c0 = block_excl<NT>(my_ctas, total_ctas, s_w);
   if (cta >= c0 && cta < c0 + my_ctas) {
     for (int g = g_lo; g < g_hi; ++g) {
       const int n = group_ctas(group_pages(a, g), total_pages, a.target);
@@ -167,166 +241,205 @@ __global__ __launch_bounds__(kThreads) void mqa_logits_decode_kernel(const Decod
     }
   }
 
-  // ---- mask words past group `cta`'s pages (grid >= groups, so every group has an owner) ----
-  if (cta < a.n_groups) {
-    const int p0 = group_pages(a, cta);
-    const int words = (a.bt_pages - p0) * 4;
-    for (int r = 0; r < R; ++r) {
-      int16_t* m = a.mask + static_cast<int64_t>(cta * R + r) * a.mask_stride + p0 * 4;
-      for (int i = tid; i < words; i += kThreads) m[i] = 0;
+  if (a.zero_ws != nullptr) {
+    // the top-k's pass-1 workspace [histograms rows*4096 | counters rows*4096 | counts rows*2],
+    // a share per CTA: the histograms in 16-B stores, counter words 0..2 and the counts per row
+    const int64_t units = a.batch * (kBins / 4);
+    const int64_t u0 = units * cta / gridDim.x;
+    const int64_t u1 = units * (cta + 1) / gridDim.x;
+    int4* h4 = reinterpret_cast<int4*>(a.zero_ws);
+    for (int64_t u = u0 + tid; u < u1; u += NT) h4[u] = make_int4(0, 0, 0, 0);
+    for (int64_t rr = cta; rr < a.batch; rr += gridDim.x) {
+      if (tid < 3) a.zero_ws[(a.batch + rr) * kBins + tid] = 0;
+      if (tid < 2) a.zero_ws[2 * a.batch * kBins + 2 * rr + tid] = 0;
     }
   }
   __syncthreads();
   const int grp = s_assign[0];
   if (grp < 0) return;  // uniform: no pages for this CTA
-  const int j = s_assign[1];
+  const int jc = s_assign[1];
   const int nj = s_assign[2];
 
+  // wave = row r of the group x stream s: stream s takes the CTA's pages s, s + S, ...; its R
+  // waves share each page through an LDS slot, one row each.
+  const int r = wave / S;
+  const int s = wave % S;
   const int row0 = grp * R;
+  const int row = row0 + r;
   const int group_row = (row0 / a.group) * a.group;
-  int len[R];
-  int hlim[R];
   int max_len = 0;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    len[r] = clamp_len(a.ctx[row0 + r], a.width);
-    max_len = max(max_len, len[r]);
-    hlim[r] = 0;
-    if constexpr (kHist) {
-      int h = a.hist_lens[row0 + r];
-      h = h < a.width ? h : a.width;
-      hlim[r] = h > kTopK ? h : 0;
-    }
+  for (int q = 0; q < R; ++q) max_len = max(max_len, clamp_len(a.ctx[row0 + q], a.width));
+  const int len = clamp_len(a.ctx[row], a.width);
+  int hlim = 0;
+  if constexpr (kHist) {
+    int h = a.hist_lens[row];
+    h = h < a.width ? h : a.width;
+    hlim = h > kTopK ? h : 0;
   }
   const int pages = (max_len + kPage - 1) / kPage;
-  const int p_begin = static_cast<int>(static_cast<int64_t>(pages) * j / nj);
-  const int p_end = static_cast<int>(static_cast<int64_t>(pages) * (j + 1) / nj);
-  const int n_local = p_end - p_begin;  // <= kMaxCtaPages by the host's choice of target
-
+  const int p_begin = static_cast<int>(static_cast<int64_t>(pages) * jc / nj);
+  const int p_end = static_cast<int>(static_cast<int64_t>(pages) * (jc + 1) / nj);
+  const int n_local = p_end - p_begin;  // <= Sh::kMaxPages by the host's choice of target
   const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride + p_begin;
-  for (int i = tid; i < n_local; i += kThreads) s_bt[i] = btr[i];
-  if constexpr (kHist) {
-    for (int i = tid; i < R * kBins; i += kThreads) s_hist[i] = 0;
-    if (tid < 2 * R) s_cnt[tid] = 0;
-  }
-  __syncthreads();
 
-  // q / w fragments (see header comment for the lane mapping).
-  i32x8 qf[R][HT];
-  float wf[R][HT * 4];
+  // the first page(s) of every stream in flight first, straight from the block table
+  if (s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[s]) * a.page_stride, s_slot0[s], r, lane);
+  if constexpr (NS > 2) {
+    if (S + s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[S + s]) * a.page_stride, s_slot1[s], r, lane);
+  }
+
+  // q / w fragments of this wave's row: lane l holds head ht*16 + l%16, bytes (l/16)*32 .. +32,
+  // and the weights of heads ht*16 + 4*(l/16) + e, the rows of the MFMA result it holds.
+  i32x8 qf[HT];
+  float wf[HT * 4];
+  {
+    const uint8_t* qr = a.q8 + static_cast<int64_t>(row) * H * kHeadDim + (lane & 15) * kHeadDim + (lane >> 4) * 32;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint8_t* qr = a.q8 + static_cast<int64_t>(row0 + r) * H * kHeadDim + (lane & 15) * kHeadDim + (lane >> 4) * 32;
-#pragma unroll
-    for (int ht = 0; ht < HT; ++ht) qf[r][ht] = load_frag(qr + ht * 16 * kHeadDim);
-    const float* wr = a.w + static_cast<int64_t>(row0 + r) * H + 4 * (lane >> 4);
+    for (int ht = 0; ht < HT; ++ht) qf[ht] = load_frag(qr + ht * 16 * kHeadDim);
+    const float* wr = a.w + static_cast<int64_t>(row) * H + 4 * (lane >> 4);
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wf[r][ht * 4 + i] = wr[ht * 16 + i];
+      for (int e = 0; e < 4; ++e) wf[ht * 4 + e] = wr[ht * 16 + e];
     }
   }
 
-  int nz[R], pos[R];
+  for (int i = tid; i < n_local; i += NT) s_bt[i] = btr[i];
+  if constexpr (kHist) {
+    for (int i = tid; i < R * kBins / 2; i += NT) s_hist[i] = 0;
+    if (tid < 2 * R) s_cnt[tid] = 0;
+  }
+  // Mask words of the group's rows past its pages (no CTA scores them) are zeroed by the
+  // group's CTAs, a share each: one 8-B store per page and row when the layout allows it.
+  {
+    const int tail = a.bt_pages - pages;
+    const int units = R * tail;
+    const int u0 = static_cast<int>(static_cast<int64_t>(units) * jc / nj);
+    const int u1 = static_cast<int>(static_cast<int64_t>(units) * (jc + 1) / nj);
+    const bool wide = (reinterpret_cast<uintptr_t>(a.mask) & 7u) == 0 && (a.mask_stride & 3) == 0;
+    for (int u = u0 + tid; u < u1; u += NT) {
+      const int rr = u / tail;
+      int16_t* m = a.mask + static_cast<int64_t>(row0 + rr) * a.mask_stride + (pages + u - rr * tail) * 4;
+      if (wide) {
+        *reinterpret_cast<uint64_t*>(m) = 0;
+      } else {
 #pragma unroll
-  for (int r = 0; r < R; ++r) nz[r] = pos[r] = 0;
+        for (int e = 0; e < 4; ++e) m[e] = 0;
+      }
+    }
+  }
+  __syncthreads();
 
-  // Scores one page held in registers: MFMA tiles, weighted ReLU head sum, mask / logits stores
-  // and the fused pass-1 histogram.
-  auto score_page = [&](int i, const PageRegs& cur) {
-    float val[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) val[r] = 0.0f;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        f32x4 acc[HT];
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma_fp8(qf[r][ht], cur.k[st], f32x4{0.f, 0.f, 0.f, 0.f});
-        float s = 0.0f;
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) s += relu_bits(acc[ht][e]) * wf[r][ht * 4 + e];
-        }
-        s = sum_lanes_16_32(s);
-        val[r] = (lane >> 4) == st ? s : val[r];
+  int nz = 0, pos = 0;
+  const int n_steps = (n_local + S - 1) / S;  // block-uniform
+  const int t_lo = lane & 15;
+  const int p0 = (lane >> 4) * 2;
+
+  // Results of a scored page are written at the start of the next step, before that step's DMA
+  // is issued: the wait at the top of a step then finds the stores older than the DMA, and the
+  // LDS histogram atomics never have a DMA in flight to wait for.
+  int pend_p = -1;  // page of the held results (wave-uniform), -1: none
+  float pend_v = 0.0f;
+  uint64_t pend_bits = 0;
+  auto flush = [&]() {
+    if (pend_p < 0) return;
+    const int token = pend_p * kPage + lane;
+    if (lane < 4)
+      a.mask[static_cast<int64_t>(row) * a.mask_stride + pend_p * 4 + lane] =
+          static_cast<int16_t>((pend_bits >> (16 * lane)) & 0xFFFFu);
+    if (token < len) a.logits[static_cast<int64_t>(row) * a.logits_stride + token] = pend_v;
+    if constexpr (kHist) {
+      if (((pend_bits >> lane) & 1u) && token < hlim) {
+        const uint32_t key = float_key(pend_v);
+        atomicAdd(&s_hist[r * (kBins / 2) + static_cast<int>(key >> 21)], 1u << ((key >> 16) & 16u));
+        ++nz;
+        pos += key > kZeroKey;
       }
     }
-    const int p = p_begin + i;
-    const int token = p * kPage + lane;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = val[r] * cur.scale;
-      const bool live = token < len[r];
-      const bool keep = live && __float_as_uint(v) != 0u;
-      const uint64_t bits = __ballot(keep);
-      const int64_t row = row0 + r;
-      if (lane < 4) a.mask[row * a.mask_stride + p * 4 + lane] = static_cast<int16_t>((bits >> (16 * lane)) & 0xFFFFu);
-      if (live) a.logits[row * a.logits_stride + token] = v;
-      if constexpr (kHist) {
-        if (keep && token < hlim[r]) {
-          const uint32_t key = float_key(v);
-          atomicAdd(&s_hist[r * kBins + static_cast<int>(key >> 20)], 1);
-          ++nz[r];
-          pos[r] += key > kZeroKey;
-        }
-      }
-    }
+    pend_p = -1;
   };
 
-  // Pages w, w+4, ... with two pages in flight while one is scored.  The loop is unrolled over
-  // three register sets so that no set is copied (a copy would wait for its loads), and the
-  // prefetches are unconditional -- past the end they re-read the wave's last page, an L2 hit --
-  // so the in-order load counter only ever waits for the page being scored.
-  constexpr int kStepP = kWavesPerCta;
-  int i = wave;
-  if (i < n_local) {
-    const int last = wave + (n_local - 1 - wave) / kStepP * kStepP;
-    auto page_of = [&](int k) { return s_bt[k < last ? k : last]; };
-    PageRegs pa, pb, pc;
-    load_page(a.kv, a.page_stride, page_of(i), lane, pa);
-    load_page(a.kv, a.page_stride, page_of(i + kStepP), lane, pb);
-    while (true) {
-      load_page(a.kv, a.page_stride, page_of(i + 2 * kStepP), lane, pc);
-      score_page(i, pa);
-      i += kStepP;
-      if (i >= n_local) break;
-      load_page(a.kv, a.page_stride, page_of(i + 2 * kStepP), lane, pa);
-      score_page(i, pb);
-      i += kStepP;
-      if (i >= n_local) break;
-      load_page(a.kv, a.page_stride, page_of(i + 2 * kStepP), lane, pb);
-      score_page(i, pc);
-      i += kStepP;
-      if (i >= n_local) break;
+  // One step: page i of this stream is in `cur`; page i + (NS - 1) S is sent to `nxt`.
+  const int n_dma = dma_ops<R>(r);
+  auto step = [&](int k, uint8_t* cur, uint8_t* nxt) {
+    const int i = k * S + s;  // this stream's page (local index)
+    // this wave's share of page i has landed: the only VMEM ops issued after it are the DMAs of
+    // the pages still ahead of it (NS = 3: page i + S, if it exists).  The barrier publishes
+    // every wave's share and retires the readers of `nxt` from the previous step.
+    if (NS > 2 && i + S < n_local) wait_vmcnt(n_dma);
+    else wait_vmcnt(0);
+    // a bare s_barrier: __syncthreads' release fence would wait for every LDS DMA in flight
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS histogram updates are done
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    flush();
+    if (i + (NS - 1) * S < n_local)
+      dma_page<R>(a.kv + static_cast<int64_t>(s_bt[i + (NS - 1) * S]) * a.page_stride, nxt, r, lane);
+    if (i >= n_local) return;  // stream-uniform (the stream still takes part in the barriers)
+    const float scale = reinterpret_cast<const float*>(cur + kPageFp8Bytes)[lane];
+    float val = 0.0f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const i32x8 kf = lds_frag(cur, st * 16 + t_lo, p0);
+      f32x4 acc[HT];
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma_fp8(qf[ht], kf, f32x4{0.f, 0.f, 0.f, 0.f});
+      float sum = 0.0f;
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += relu_bits(acc[ht][e]) * wf[ht * 4 + e];
+      }
+      sum = sum_lanes_16_32(sum);
+      val = (lane >> 4) == st ? sum : val;
+    }
+    const int p = p_begin + i;
+    const float v = val * scale;
+    pend_p = p;
+    pend_v = v;
+    pend_bits = __ballot(p * kPage + lane < len && __float_as_uint(v) != 0u);
+  };
+  // the two slots of a stream are distinct LDS objects, so the compiler can tell that the
+  // reads of one do not wait for the DMA into the other
+  if constexpr (NS == 2) {
+    for (int k = 0; k < n_steps; k += 2) {
+      step(k, s_slot0[s], s_slot1[s]);
+      if (k + 1 < n_steps) step(k + 1, s_slot1[s], s_slot0[s]);
+    }
+  } else {
+    for (int k = 0; k < n_steps; k += 3) {
+      step(k, s_slot0[s], s_slot2[s]);
+      if (k + 1 < n_steps) step(k + 1, s_slot1[s], s_slot0[s]);
+      if (k + 2 < n_steps) step(k + 2, s_slot2[s], s_slot1[s]);
     }
   }
+  flush();
 
   if constexpr (kHist) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = wave_sum(nz[r]);
-      const int q = wave_sum(pos[r]);
-      if (lane == 0 && n) {
-        atomicAdd(&s_cnt[2 * r], n);
-        atomicAdd(&s_cnt[2 * r + 1], q);
-      }
+    const int n = wave_sum(nz);
+    const int q = wave_sum(pos);
+    if (lane == 0 && n) {
+      atomicAdd(&s_cnt[2 * r], n);
+      atomicAdd(&s_cnt[2 * r + 1], q);
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (hlim[r] == 0) continue;
-      int32_t* gh = a.hist_ws + static_cast<int64_t>(row0 + r) * kBins;
-      int32_t* gcnt = a.hist_ws + 2 * a.batch * kBins + 2 * static_cast<int64_t>(row0 + r);
-      for (int b = tid; b < kBins; b += kThreads) {
-        const int c = s_hist[r * kBins + b];
-        if (c) atomicAdd(&gh[b], c);
+    for (int rr = 0; rr < R; ++rr) {
+      int h = a.hist_lens[row0 + rr];
+      h = h < a.width ? h : a.width;
+      if (h <= kTopK) continue;  // block-uniform
+      int32_t* gh = a.hist_ws + static_cast<int64_t>(row0 + rr) * kBins;
+      int32_t* gcnt = a.hist_ws + 2 * a.batch * kBins + 2 * static_cast<int64_t>(row0 + rr);
+      for (int wd = tid; wd < kBins / 2; wd += NT) {
+        const uint32_t c = s_hist[rr * (kBins / 2) + wd];
+        if (c & 0xFFFFu) atomicAdd(&gh[2 * wd], static_cast<int>(c & 0xFFFFu));
+        if (c >> 16) atomicAdd(&gh[2 * wd + 1], static_cast<int>(c >> 16));
       }
       if (tid == 0) {
-        const int n = s_cnt[2 * r];
-        const int q = s_cnt[2 * r + 1];
+        const int n = s_cnt[2 * rr];
+        const int q = s_cnt[2 * rr + 1];
         if (n) {
           atomicSub(&gh[kZeroBin], n);
           atomicSub(&gcnt[1], n);
@@ -360,8 +473,8 @@ __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __res
 
 template <int H, int R, bool kHist>
 void launch_one(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
-  const size_t lds = kHist ? static_cast<size_t>(R) * kBins * sizeof(int) : 0;
-  hipLaunchKernelGGL((mqa_logits_decode_kernel<H, R, kHist>), dim3(grid), dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((mqa_logits_decode_kernel<H, R, kHist>), dim3(grid), dim3(Shape<R, kHist>::kThreads), 0, stream,
+                     a);
 }
 
 template <int H, bool kHist>
@@ -376,6 +489,19 @@ void launch_r(const DecodeArgs& a, int R, uint32_t grid, hipStream_t stream) {
   }
 }
 
+// (CTAs per CU, pages per CTA) of a launch shape, on the host.
+void shape_host(int R, bool hist, int& ctas_per_cu, int& max_pages) {
+  switch (hist ? R + 4 : R) {
+    case 1: ctas_per_cu = Shape<1, false>::kCtasPerCu; max_pages = Shape<1, false>::kMaxPages; break;
+    case 2: ctas_per_cu = Shape<2, false>::kCtasPerCu; max_pages = Shape<2, false>::kMaxPages; break;
+    case 3: ctas_per_cu = Shape<3, false>::kCtasPerCu; max_pages = Shape<3, false>::kMaxPages; break;
+    case 4: ctas_per_cu = Shape<4, false>::kCtasPerCu; max_pages = Shape<4, false>::kMaxPages; break;
+    case 5: ctas_per_cu = Shape<1, true>::kCtasPerCu; max_pages = Shape<1, true>::kMaxPages; break;
+    case 6: ctas_per_cu = Shape<2, true>::kCtasPerCu; max_pages = Shape<2, true>::kMaxPages; break;
+    default: ctas_per_cu = Shape<3, true>::kCtasPerCu; max_pages = Shape<3, true>::kMaxPages; break;
+  }
+}
+
 }  // namespace
 }  // namespace dsa
 
@@ -386,7 +512,8 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
                                      const int32_t* context_lens, const int32_t* block_table, int64_t bt_stride,
                                      int64_t bt_pages, float* logits, int64_t logits_stride, int16_t* mask,
                                      int64_t mask_stride, int rows_per_cta, int target_ctas,
-                                     const int32_t* hist_lens, int32_t* hist_ws, hipStream_t stream) {
+                                     const int32_t* hist_lens, int32_t* hist_ws, int fuse_pass1,
+                                     hipStream_t stream) {
   DSA_REQUIRE(heads == 32 || heads == 64, "dsa_mqa_logits_decode: heads must be 32 or 64 (got %d)", heads);
   DSA_REQUIRE(batch >= 0 && group_size >= 1, "dsa_mqa_logits_decode: batch must be >= 0 and group_size >= 1");
   DSA_REQUIRE(batch % group_size == 0, "dsa_mqa_logits_decode: batch must be a multiple of group_size");
@@ -405,26 +532,30 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   const int64_t width = bt_pages * kPage;
   DSA_REQUIRE(bt_stride >= bt_pages && logits_stride >= width && mask_stride >= width / 16,
               "dsa_mqa_logits_decode: strides smaller than the block table capacity");
-  DSA_REQUIRE((hist_lens == nullptr) == (hist_ws == nullptr),
-              "dsa_mqa_logits_decode: hist_lens and hist_ws go together");
-  const bool hist = hist_ws != nullptr;  // 32-bit LDS counters: no limit on tokens per CTA
+  DSA_REQUIRE(!fuse_pass1 || (hist_lens != nullptr && hist_ws != nullptr),
+              "dsa_mqa_logits_decode: fuse_pass1 needs hist_lens and hist_ws");
+  DSA_REQUIRE(hist_ws == nullptr || (reinterpret_cast<uintptr_t>(hist_ws) & 15u) == 0,
+              "dsa_mqa_logits_decode: hist_ws must be 16-B aligned");
+  const bool hist = fuse_pass1 != 0;
   DSA_REQUIRE(!hist || rows_per_cta <= 3,
-              "dsa_mqa_logits_decode: the fused histogram needs rows_per_cta <= 3 (16 KB of LDS per row)");
+              "dsa_mqa_logits_decode: the fused histogram needs rows_per_cta <= 3 (8 KB of LDS per row)");
   const int64_t n_groups = batch / rows_per_cta;
   DSA_REQUIRE(n_groups <= 0x3FFFFFFF, "dsa_mqa_logits_decode: batch too large");
+  int ctas_per_cu = 1, max_cta_pages = 1;
+  shape_host(rows_per_cta, hist, ctas_per_cu, max_cta_pages);
   if (target_ctas <= 0) {
-    // Two CTAs fit a CU; the per-group rounding adds up to one CTA per group, so aim below the
-    // resident count by the group count to finish in one round of CTAs.
+    // All CTAs resident at once: the per-group rounding adds up to one CTA per group, so aim
+    // below the resident count by the group count.
     int n_cu = 0;
     const int st = dsa_device_cu_count(&n_cu);
     if (st != DSA_OK) return st;
-    const int64_t slots = 2 * static_cast<int64_t>(n_cu);
-    target_ctas = static_cast<int>(slots - n_groups > n_cu ? slots - n_groups : n_cu);
+    const int64_t slots = ctas_per_cu * static_cast<int64_t>(n_cu);
+    target_ctas = static_cast<int>(slots - n_groups > slots / 2 ? slots - n_groups : slots / 2);
   }
-  // Keep every CTA's page slice within the LDS block-table stage: P / T <= kMaxCtaPages.
+  // Keep every CTA's page slice within the LDS block-table stage: P / T <= max_pages.
   const int64_t max_pages = n_groups * bt_pages;
   int64_t target = target_ctas;
-  if (target * kMaxCtaPages < max_pages) target = (max_pages + kMaxCtaPages - 1) / kMaxCtaPages;
+  if (target * max_cta_pages < max_pages) target = (max_pages + max_cta_pages - 1) / max_cta_pages;
   const int64_t grid = target + n_groups;
   DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_mqa_logits_decode: grid too large");
 
@@ -446,8 +577,9 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   a.R = rows_per_cta;
   a.n_groups = static_cast<int>(n_groups);
   a.target = static_cast<int>(target);
-  a.hist_lens = hist_lens;
-  a.hist_ws = hist_ws;
+  a.hist_lens = hist ? hist_lens : nullptr;
+  a.hist_ws = hist ? hist_ws : nullptr;
+  a.zero_ws = hist ? nullptr : hist_ws;
   a.batch = batch;
 
   if (hist) {

@@ -31,7 +31,6 @@ namespace {
 
 constexpr int kTk = 1024;   // threads of the one-CTA-per-row kernel
 constexpr int kTs = 512;    // threads of the split collect / resolve CTAs
-constexpr int kTh = 256;    // threads of the split pass-1 CTAs
 constexpr int kCapC = 8192; // candidates the one-CTA-per-row kernel resolves in LDS
 constexpr int kCapS = 4096; // candidates of a row the split kernel resolves in LDS
 constexpr int kMaxSplit = 64;
@@ -264,8 +263,8 @@ __device__ __forceinline__ void stream_batches(const RowSrc& rr, int b, int n_ba
   }
 }
 
-// Pass 1 over [begin, end) (end > begin) of the row into an LDS histogram (zeros counted, not
-// binned); returns the range's positive / zero counts (block-uniform).
+// Pass 1 over [begin, end) (end > begin) of the row into the LDS histogram `hist` (zeroed here;
+// zeros counted, not binned); returns the range's positive / zero counts (block-uniform).
 template <bool kVec, int NT>
 __device__ void pass_hist(const RowSrc& r, int begin, int end, int* hist, int* s_red, int& pos, int& zeros) {
   constexpr int kStep = NT * 4 * kUnroll;
@@ -275,6 +274,8 @@ __device__ void pass_hist(const RowSrc& r, int begin, int end, int* hist, int* s
   Batch x0, x1;
   load_batch<kVec, NT>(rr, b0, x0);
   load_batch<kVec, NT>(rr, b0 + kStep, x1);
+  zero_lds<NT>(hist, kBins);  // while the first batches are in flight
+  __syncthreads();
   int zc = 0, pc = 0;
   stream_batches<kVec, NT>(rr, b0, (end - begin + kStep - 1) / kStep, x0, x1, [&](int b, const Batch& x) {
 #pragma unroll
@@ -695,8 +696,6 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
     }
   } else {
     int pos, zeros;
-    zero_lds<kTk>(L.hist, kBins);
-    __syncthreads();
     pass_hist<kVec, kTk>(r, 0, len, L.hist, L.red, pos, zeros);
     if (threadIdx.x == 0 && zeros) L.hist[kZeroBin] += zeros;
     load_batch<kVec, kTk>(r, b0, x0);
@@ -723,13 +722,7 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Split variant.  Slices are multiples of 2048 tokens; CTAs are slice-major (blockIdx = s *
-// rows + row), so the slices of consecutive rows spread over the XCDs.
-__device__ __forceinline__ int slice_len(int len, int S) {
-  const int per = (len + S - 1) / S;
-  return (per + 2047) / 2048 * 2048;
-}
-
+// Split variant.  CTAs cover balanced slices of the rows (split_assign).
 // Zeroes the pass-1 histogram, counts and per-row counters of the split path.
 __global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ ghist, int32_t* __restrict__ gcnt,
                                                         int32_t* __restrict__ ctr, int64_t ctr_stride) {
@@ -738,34 +731,6 @@ __global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ gh
   for (int i = threadIdx.x; i < kBins / 4; i += 256) g[i] = make_int4(0, 0, 0, 0);
   if (threadIdx.x < 2) gcnt[2 * row + threadIdx.x] = 0;
   if (threadIdx.x < 3) ctr[row * ctr_stride + threadIdx.x] = 0;
-}
-
-// Pass 1 of one slice into the row's global histogram / counts.
-template <bool kVec>
-__global__ __launch_bounds__(kTh) void topk_split_hist_kernel(const TopkArgs a) {
-  __shared__ int hist[kBins];
-  __shared__ int red[kTh / kWave];
-  const int row = blockIdx.x % a.rows;
-  const int s = blockIdx.x / a.rows;
-  const int len = row_len(a, row);
-  if (len <= kTopK) return;
-  const int sl = slice_len(len, a.S);
-  const int begin = s * sl;
-  if (begin >= len) return;
-  const int end = min(begin + sl, len);
-  zero_lds<kTh>(hist, kBins);
-  __syncthreads();
-  int pos, zeros;
-  pass_hist<kVec, kTh>(row_src(a, row, len), begin, end, hist, red, pos, zeros);
-  int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
-  for (int i = threadIdx.x; i < kBins; i += kTh) {
-    const int c = hist[i] + (i == kZeroBin ? zeros : 0);
-    if (c) atomicAdd(&gh[i], c);
-  }
-  if (threadIdx.x == 0) {
-    if (pos) atomicAdd(&a.gcnt[2 * row], pos);
-    if (zeros) atomicAdd(&a.gcnt[2 * row + 1], zeros);
-  }
 }
 
 struct SplitLds {
@@ -784,11 +749,20 @@ struct SplitLds {
   int slot[3];
 };
 
+struct HistLds {
+  int hist[kBins];
+  int red[kTs / kWave];
+  int wtot[kTs / kWave];
+  long long lsum[kTs / kWave];
+  int slot[3];
+};
+
 // Balanced split: row r gets c_r = ceil(len_r * T / L) CTAs (L = the summed lengths of the rows
 // longer than 2048; a row of <= 2048 tokens gets one CTA, which copies it), in row order, so
 // that every CTA streams about L / T tokens whatever the length mix; the sum is <= T + rows, the
 // grid.  Needs rows <= kTs.  s_slot = {row (-1: none), index among the row's CTAs, c_r}.
-__device__ void split_assign(const TopkArgs& a, int T, SplitLds& L) {
+template <typename Lds>
+__device__ void split_assign(const TopkArgs& a, int T, Lds& L) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
@@ -825,6 +799,41 @@ __device__ void split_assign(const TopkArgs& a, int T, SplitLds& L) {
   __syncthreads();
 }
 
+// Slice of a row (by split_assign) this CTA covers: [begin, end) of len tokens, n_sl slices in
+// the row; false when the CTA has none.  Slices are whole 256-token blocks.
+__device__ __forceinline__ bool split_slice(int len, int c, int j, int& begin, int& end, int& n_sl) {
+  const int sl = ((len + c - 1) / c + 255) / 256 * 256;
+  begin = j * sl;
+  end = min(begin + sl, len);
+  n_sl = (len + sl - 1) / sl;
+  return begin < len;
+}
+
+// Pass 1 of one balanced slice (the split kernel's slices) into the row's global histogram and
+// positive / zero counts, which start at zero.
+template <bool kVec>
+__global__ __launch_bounds__(kTs) void topk_split_hist_kernel(const TopkArgs a) {
+  __shared__ HistLds L;
+  split_assign(a, a.T, L);
+  const int row = L.slot[0];
+  if (row < 0) return;  // block-uniform
+  const int len = row_len(a, row);
+  if (len <= kTopK) return;
+  int begin, end, n_sl;
+  if (!split_slice(len, L.slot[2], L.slot[1], begin, end, n_sl)) return;
+  int pos, zeros;
+  pass_hist<kVec, kTs>(row_src(a, row, len), begin, end, L.hist, L.red, pos, zeros);
+  int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
+  for (int i = threadIdx.x; i < kBins; i += kTs) {
+    const int c = L.hist[i] + (i == kZeroBin ? zeros : 0);
+    if (c) atomicAdd(&gh[i], c);
+  }
+  if (threadIdx.x == 0) {
+    if (pos) atomicAdd(&a.gcnt[2 * row], pos);
+    if (zeros) atomicAdd(&a.gcnt[2 * row + 1], zeros);
+  }
+}
+
 // Per slice (balanced over the rows by split_assign): pass-1 threshold (from the row's
 // histogram), unordered collection, then the A
 // tokens go straight to the output and the candidates to the row's published list, both at
@@ -844,12 +853,8 @@ __global__ __launch_bounds__(kTs) void topk_split_kernel(const TopkArgs a) {
     copy_short_row<kTs>(pt_row(a, row), a.out + static_cast<int64_t>(row) * kTopK, len);
     return;
   }
-  const int c = L.slot[2];
-  const int sl = ((len + c - 1) / c + 255) / 256 * 256;  // slices of whole 256-token blocks
-  const int begin = L.slot[1] * sl;
-  if (begin >= len) return;
-  const int end = min(begin + sl, len);
-  const int n_sl = (len + sl - 1) / sl;
+  int begin, end, n_sl;
+  if (!split_slice(len, L.slot[2], L.slot[1], begin, end, n_sl)) return;
 
   // pass-1 slots (8 bins per thread) and counts first, then the first two batches
   const int4* gh4 = reinterpret_cast<const int4*>(a.ghist + static_cast<int64_t>(row) * kBins);
@@ -985,7 +990,8 @@ WsLayout ws_layout(int64_t rows) {
 int topk_common(const float* score, int64_t score_stride, int64_t width, const int16_t* mask, int64_t mask_stride,
                 const int32_t* lengths, int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
                 const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu, int32_t* pre_hist,
-                void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream, const char* who) {
+                bool pass1_done, void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream,
+                const char* who) {
   DSA_REQUIRE(rows >= 0 && rows <= 0x7FFFFFFF, "%s: rows out of range", who);
   DSA_REQUIRE(width >= 0 && width <= 0x7FFFFFFF, "%s: width out of range", who);
   if (rows == 0) return ok();
@@ -1028,7 +1034,7 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
     a.gcnt = pre_hist + 2 * rows * kBins;
   }
   if (S <= 1) {
-    if (pre_hist) {
+    if (pre_hist && pass1_done) {
       if (vec) hipLaunchKernelGGL((topk_single_kernel<true, true>), grid_rows, dim3(kTk), 0, stream, a);
       else hipLaunchKernelGGL((topk_single_kernel<false, true>), grid_rows, dim3(kTk), 0, stream, a);
     } else {
@@ -1050,15 +1056,13 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
   }
   a.c_keys = reinterpret_cast<uint32_t*>(ws + l.c_keys);
   a.c_tok = reinterpret_cast<int32_t*>(ws + l.c_tok);
-  const dim3 grid_split(static_cast<uint32_t>(rows * S));
-  const int T = split_target(rows, S, n_cu);
-  if (!pre_hist) {
-    hipLaunchKernelGGL(topk_zero_kernel, grid_rows, dim3(256), 0, stream, a.ghist, a.gcnt, a.ctr, a.ctr_stride);
-    if (vec) hipLaunchKernelGGL((topk_split_hist_kernel<true>), grid_split, dim3(kTh), 0, stream, a);
-    else hipLaunchKernelGGL((topk_split_hist_kernel<false>), grid_split, dim3(kTh), 0, stream, a);
+  a.T = split_target(rows, S, n_cu);
+  const dim3 grid_bal(static_cast<uint32_t>(a.T + rows));
+  if (!pre_hist) hipLaunchKernelGGL(topk_zero_kernel, grid_rows, dim3(256), 0, stream, a.ghist, a.gcnt, a.ctr, a.ctr_stride);
+  if (!pass1_done) {
+    if (vec) hipLaunchKernelGGL((topk_split_hist_kernel<true>), grid_bal, dim3(kTs), 0, stream, a);
+    else hipLaunchKernelGGL((topk_split_hist_kernel<false>), grid_bal, dim3(kTs), 0, stream, a);
   }
-  a.T = T;
-  const dim3 grid_bal(static_cast<uint32_t>(T + rows));
   if (vec) hipLaunchKernelGGL((topk_split_kernel<true>), grid_bal, dim3(kTs), 0, stream, a);
   else hipLaunchKernelGGL((topk_split_kernel<false>), grid_bal, dim3(kTs), 0, stream, a);
   return check_launch(who);
@@ -1081,7 +1085,7 @@ extern "C" int dsa_topk_transform(const float* score, int64_t score_stride, int6
                                   const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
                                   void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream) {
   return topk_common(score, score_stride, width, mask, mask_stride, lengths, rows, page_table, pt_stride, pt_cols,
-                     cu_seqlens_q, n_req, max_splits, n_cu, nullptr, workspace, workspace_bytes, out, stream,
+                     cu_seqlens_q, n_req, max_splits, n_cu, nullptr, false, workspace, workspace_bytes, out, stream,
                      "dsa_topk_transform");
 }
 
@@ -1089,10 +1093,10 @@ extern "C" int dsa_topk_transform_pre(const float* score, int64_t score_stride, 
                                       int64_t mask_stride, const int32_t* lengths, int64_t rows,
                                       const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
                                       const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
-                                      int32_t* hist_ws, void* workspace, size_t workspace_bytes, int32_t* out,
-                                      hipStream_t stream) {
+                                      int32_t* hist_ws, int pass1_done, void* workspace, size_t workspace_bytes,
+                                      int32_t* out, hipStream_t stream) {
   DSA_REQUIRE(hist_ws != nullptr, "dsa_topk_transform_pre: hist_ws is null");
   return topk_common(score, score_stride, width, mask, mask_stride, lengths, rows, page_table, pt_stride, pt_cols,
-                     cu_seqlens_q, n_req, max_splits, n_cu, hist_ws, workspace, workspace_bytes, out, stream,
-                     "dsa_topk_transform_pre");
+                     cu_seqlens_q, n_req, max_splits, n_cu, hist_ws, pass1_done != 0, workspace, workspace_bytes, out,
+                     stream, "dsa_topk_transform_pre");
 }

@@ -25,13 +25,16 @@ _TOPK_SPLITS = int(os.environ.get("HCU_TOPK_SPLITS", "8"))
 # HCU_MQA_PCTAS[_G1]: CTAs the K pages of grouped [single] rows are spread over (each CTA streams a
 # slice of one request); <= 0 uses twice the CU count.  HCU_MQA_RPC: rows sharing one K stream
 # for groups (must divide the group).
-# HCU_MQA_HIST_MAX_ROWS: build the top-k pass-1 histogram inside the logits kernel up to this
-# many rows (the top-k then skips its own pass 1).
+# HCU_MQA_HIST_MAX_ROWS: up to this many rows, mqa_logits(..., hist_lens) hands the paired top-k a
+# pass-1 workspace that it zeroed (saving the top-k's zeroing launch); HCU_MQA_FUSED_PASS1=1
+# builds pass 1 inside the logits kernel instead (slower on gfx950: its LDS histogram lowers the
+# logits kernel's occupancy).
 _MQA_PCTAS = int(os.environ.get("HCU_MQA_PCTAS", "0"))
 _MQA_PCTAS_G1 = int(os.environ.get("HCU_MQA_PCTAS_G1", str(_MQA_PCTAS)))
 _MQA_RPC = int(os.environ.get("HCU_MQA_RPC", "2"))
 _MQA_HIST_MAX_ROWS = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS", "256"))
-_MQA_HIST = None  # (logits, hist_lens, zws) of the last mqa_logits with a fused histogram
+_MQA_FUSED_PASS1 = os.environ.get("HCU_MQA_FUSED_PASS1", "0") == "1"
+_MQA_HIST = None  # (logits, hist_lens, zws, pass1_done) of the last mqa_logits with hist_lens
 _HEADS = (32, 64)
 
 
@@ -44,9 +47,9 @@ def sparse_mask_topk_transform(score, nonzero_mask, lengths, page_table_size_1, 
     if st is not None:
         _MQA_HIST = None
         if st[0] is score and st[1].data_ptr() == lengths.data_ptr() and st[1].shape == lengths.shape:
-            # pass 1 (histogram) was built by mqa_logits(..., hist_lens=lengths)
+            # the pass-1 workspace came from mqa_logits(..., hist_lens=lengths)
             return _C.sparse_mask_topk_transform_split_pre(score, nonzero_mask, lengths, page_table_size_1,
-                                                           cu_seqlens_q, topk, _TOPK_SPLITS, st[2])
+                                                           cu_seqlens_q, topk, _TOPK_SPLITS, st[2], st[3])
     if _TOPK_IMPL == "single":
         return _C.sparse_mask_topk_transform(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk)
     return _C.sparse_mask_topk_transform_split(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk,
@@ -81,7 +84,7 @@ def mqa_logits(q, kv_cache, weights, context_lens, block_table, max_context_len,
     (reference hcu_ops/hcu_ops/__init__.py:82-105).
 
     hist_lens: lengths of the paired sparse_mask_topk_transform; when that call will split rows,
-    its pass-1 histogram is built here and consumed by it."""
+    its pass-1 workspace is prepared here (zeroed, or filled when HCU_MQA_FUSED_PASS1=1)."""
     global _MQA_HIST
     rows = q.shape[0]
     if persistent_ctas is None:
@@ -91,10 +94,11 @@ def mqa_logits(q, kv_cache, weights, context_lens, block_table, max_context_len,
     use_hist = (hist_lens is not None and _TOPK_IMPL == "split" and rows <= _MQA_HIST_MAX_ROWS
                 and hist_lens.dtype == torch.int32 and hist_lens.dim() == 1
                 and hist_lens.shape[0] == rows and hist_lens.is_contiguous())
+    fused = use_hist and _MQA_FUSED_PASS1 and rows_per_cta <= 3
     logits, mask, zws = _C.mqa_logits_hist(q, kv_cache, weights, context_lens.view(-1), block_table,
                                            max_context_len, group_size, persistent_ctas, rows_per_cta,
-                                           hist_lens if use_hist else None)
-    _MQA_HIST = (logits, hist_lens, zws) if use_hist else None
+                                           hist_lens if use_hist else None, fused)
+    _MQA_HIST = (logits, hist_lens, zws, fused) if use_hist else None
     return logits, mask
 
 

@@ -53,13 +53,16 @@ def test_contract_violations_are_rejected_on_the_host(lib):
     assert f(P(16), 8000, P(16), 4, P(16), 128, None) == 1  # page stride below 8448
     assert "8448" in _err(lib)
     g = lib.dsa_mqa_logits_decode
-    g.argtypes = [P, P, I, I64, I, P, I64, P, P, I64, I64, P, I64, P, I64, I, I, P, P, P]
-    assert g(P(16), P(16), 48, 2, 1, P(16), 8448, P(16), P(16), 4, 4, P(16), 256, P(16), 16, 1, 0, None, None,
+    g.argtypes = [P, P, I, I64, I, P, I64, P, P, I64, I64, P, I64, P, I64, I, I, P, P, I, P]
+    assert g(P(16), P(16), 48, 2, 1, P(16), 8448, P(16), P(16), 4, 4, P(16), 256, P(16), 16, 1, 0, None, None, 0,
              None) == 1
     assert "heads" in _err(lib)
-    assert g(P(16), P(16), 64, 3, 2, P(16), 8448, P(16), P(16), 4, 4, P(16), 256, P(16), 16, 1, 0, None, None,
+    assert g(P(16), P(16), 64, 3, 2, P(16), 8448, P(16), P(16), 4, 4, P(16), 256, P(16), 16, 1, 0, None, None, 0,
              None) == 1
     assert "group_size" in _err(lib)
+    assert g(P(16), P(16), 64, 2, 1, P(16), 8448, P(16), P(16), 4, 4, P(16), 256, P(16), 16, 1, 0, None, P(16), 1,
+             None) == 1
+    assert "fuse_pass1" in _err(lib)
     t = lib.dsa_topk_transform
     t.argtypes = [P, I64, I64, P, I64, P, I64, P, I64, I64, P, I64, I, I, P, ctypes.c_size_t, P, P]
     lib.dsa_topk_workspace_bytes.argtypes = [I64, I64, I, I]

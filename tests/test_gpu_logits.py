@@ -82,8 +82,10 @@ def test_decode_logits_sparse_and_negative_modes(gpu):
     _check_decode(case, lg, mask)
 
 
-@pytest.mark.parametrize("group,lens", [(1, [9000, 5000, 1500, 40000]), (2, [20000, 3000])])
-def test_decode_fused_histogram(gpu, group, lens):
+@pytest.mark.parametrize("group,lens", [(1, [9000, 5000, 1500, 40000]), (2, [20000, 3000]),
+                                        (2, [65536, 64000, 700, 0, 3000, 2049])])
+def test_decode_fused_histogram(gpu, monkeypatch, group, lens):
+    monkeypatch.setattr(hcu_ops, "_MQA_FUSED_PASS1", True)
     case = wl.decode_case(13, lens, group=group, heads=64)
     _, _, lg, mask = _run_decode(case, gpu, hist=True)
     zws = hcu_ops._MQA_HIST[2].cpu().numpy() if hcu_ops._MQA_HIST is not None else None
@@ -93,6 +95,21 @@ def test_decode_fused_histogram(gpu, group, lens):
     B = case.rows
     assert np.array_equal(zws[:B * 4096], ref[:B * 4096]), "ghist1 differs"
     assert np.array_equal(zws[2 * B * 4096:], ref[2 * B * 4096:]), "(positives, zeros) differ"
+    assert not zws[B * 4096:2 * B * 4096].reshape(B, 4096)[:, :3].any(), "split counters not zeroed"
+    _check_decode(case, lg, mask)
+
+
+@pytest.mark.parametrize("group,lens", [(1, [9000, 100, 40000]), (2, [20000, 3000, 0, 0])])
+def test_decode_pass1_workspace_zeroed(gpu, monkeypatch, group, lens):
+    """Without the fused pass 1 the logits call hands over the pass-1 workspace zeroed."""
+    monkeypatch.setattr(hcu_ops, "_MQA_FUSED_PASS1", False)
+    case = wl.decode_case(14, lens, group=group, heads=64)
+    _, _, lg, mask = _run_decode(case, gpu, hist=True)
+    assert hcu_ops._MQA_HIST is not None and hcu_ops._MQA_HIST[3] is False
+    B = case.rows
+    zws = hcu_ops._MQA_HIST[2].cpu().numpy()
+    assert not zws[:B * 4096].any() and not zws[2 * B * 4096:].any()
+    assert not zws[B * 4096:2 * B * 4096].reshape(B, 4096)[:, :3].any()
     _check_decode(case, lg, mask)
 
 

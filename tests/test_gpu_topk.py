@@ -86,21 +86,25 @@ def test_topk_dense_and_varlen(gpu):
         assert np.array_equal(sorted_rows(got.cpu().numpy()), ref), f"splits={splits}"
 
 
-def test_topk_fused_pass1_pairing(gpu):
-    """mqa_logits(hist_lens=lengths) -> sparse_mask_topk_transform consumes the fused pass 1 and
-    gives the same set as the top-k with its own pass 1 on the same logits."""
-    case = wl.decode_case(17, [30000, 12000, 4000, 1000], group=1, heads=64)
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("group,lens", [(1, [30000, 12000, 4000, 1000]), (2, [65536, 60000, 3000, 2100, 900, 20000])])
+def test_topk_pass1_pairing(gpu, monkeypatch, fused, group, lens):
+    """mqa_logits(hist_lens=lengths) -> sparse_mask_topk_transform consumes the paired pass-1
+    workspace (zeroed by the logits call, or filled by it when fused) and gives the same set as
+    the top-k with its own pass 1 on the same logits."""
+    monkeypatch.setattr(hcu_ops, "_MQA_FUSED_PASS1", fused)
+    case = wl.decode_case(17, lens, group=group, heads=64)
     gl = lambda t: t.to(gpu)
     q8, w = hcu_ops.quant_q_fp8(gl(case.q), gl(case.w))
     lens = gl(case.context_lens)
     pt = gl(case.page_table_1())
     cu = torch.arange(case.rows + 1, dtype=torch.int32, device=gpu)
-    lg, mask = hcu_ops.mqa_logits(q8.unsqueeze(1), gl(case.kv), w, lens, gl(case.block_table), case.width, 1,
+    lg, mask = hcu_ops.mqa_logits(q8.unsqueeze(1), gl(case.kv), w, lens, gl(case.block_table), case.width, group,
                                   hist_lens=lens)
-    assert hcu_ops._MQA_HIST is not None
-    fused = hcu_ops.sparse_mask_topk_transform(lg, mask, lens, pt, cu)
+    assert hcu_ops._MQA_HIST is not None and hcu_ops._MQA_HIST[3] == fused
+    paired = hcu_ops.sparse_mask_topk_transform(lg, mask, lens, pt, cu)
     assert hcu_ops._MQA_HIST is None
     plain = _C.sparse_mask_topk_transform(lg, mask, lens, pt, cu, 2048)
     ref = _oracle(lg.cpu(), mask.cpu(), case.context_lens, case.page_table_1(), case.width)
-    assert np.array_equal(sorted_rows(fused.cpu().numpy()), sorted_rows(ref))
+    assert np.array_equal(sorted_rows(paired.cpu().numpy()), sorted_rows(ref))
     assert np.array_equal(sorted_rows(plain.cpu().numpy()), sorted_rows(ref))
