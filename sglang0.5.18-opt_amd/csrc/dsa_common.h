@@ -99,6 +99,19 @@ __device__ __forceinline__ int wave_prefix_small(int c, int& total) {
   return lanes_below(b0) + 2 * lanes_below(b1) + 4 * lanes_below(b2);
 }
 
+// The same for per-lane counts in [0, 31]: five ballots.
+__device__ __forceinline__ int wave_prefix_5(int c, int& total) {
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const uint64_t b = __ballot(c & (1 << k));
+    total += __popcll(b) << k;
+    before += lanes_below(b) << k;
+  }
+  return before;
+}
+
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // max(x, +0) as one integer max on the float bits: negative floats (and -0.0) are negative

@@ -311,50 +311,52 @@ struct Stage {
 };
 
 // A = keys above bin t1 (fast path: positive keys), C = keys in bin t1 (none on the fast
-// path); wave-aggregated LDS atomics give the staging positions.
+// path).  A lane flags its (at most 16) hits of the batch in two bitmasks; one wave prefix per
+// list and one wave-aggregated LDS atomic per list and batch give every hit its staging slot.
 template <int NT>
 __device__ __forceinline__ void process_batch(const RowSrc& rr, int b, const Batch& x, const Meta& m,
                                               const Stage& st) {
+  static_assert(kUnroll * 4 <= 16, "hit masks hold 16 keys");
+  uint32_t k[kUnroll][4];
+  uint32_t fa = 0, fc = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int i0 = b + u * NT * 4;
-    uint32_t k[4];
-    const uint32_t v = quad_keys(rr, i0, x.q[u], k);
-    int na = 0, nc = 0;
-    bool fa[4], fc[4];
+    const uint32_t v = quad_keys(rr, b + u * NT * 4, x.q[u], k[u]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool valid = (v >> j) & 1u;
-      const uint32_t d = k[j] >> 20;
-      fa[j] = valid && (m.fast ? k[j] > kZeroKey : d > m.t1);
-      fc[j] = valid && !m.fast && d == m.t1;
-      na += fa[j];
-      nc += fc[j];
+      const uint32_t d = k[u][j] >> 20;
+      fa |= static_cast<uint32_t>(valid && (m.fast ? k[u][j] > kZeroKey : d > m.t1)) << (u * 4 + j);
+      fc |= static_cast<uint32_t>(valid && !m.fast && d == m.t1) << (u * 4 + j);
     }
-    int ta, tc;
-    int pa = wave_prefix_small(na, ta);
-    int pc = wave_prefix_small(nc, tc);
-    if (ta | tc) {  // wave-uniform
-      int base_a = 0, base_c = 0;
-      if (lane_id() == 0) {
-        if (ta) base_a = atomicAdd(st.n_a, ta);
-        if (tc) base_c = atomicAdd(st.n_c, tc);
-      }
-      base_a = __shfl(base_a, 0);
-      base_c = __shfl(base_c, 0);
+  }
+  int ta, tc;
+  int pa = wave_prefix_5(__popc(fa), ta);
+  int pc = wave_prefix_5(__popc(fc), tc);
+  if ((ta | tc) == 0) return;  // wave-uniform
+  int base_a = 0, base_c = 0;
+  if (lane_id() == 0) {
+    if (ta) base_a = atomicAdd(st.n_a, ta);
+    if (tc) base_c = atomicAdd(st.n_c, tc);
+  }
+  pa += uniform(base_a);
+  pc += uniform(base_c);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (fa[j]) {
-          const int idx = base_a + pa++;
-          if (idx < st.cap_a) st.a[idx] = i0 + j;
+  for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = u * 4 + j;
+      const int t = b + u * NT * 4 + j;
+      if ((fa >> e) & 1u) {
+        if (pa < st.cap_a) st.a[pa] = t;
+        ++pa;
+      }
+      if ((fc >> e) & 1u) {
+        if (pc < st.cap_c) {
+          st.ck[pc] = k[u][j];
+          st.ci[pc] = t;
         }
-        if (fc[j]) {
-          const int idx = base_c + pc++;
-          if (idx < st.cap_c) {
-            st.ck[idx] = k[j];
-            st.ci[idx] = i0 + j;
-          }
-        }
+        ++pc;
       }
     }
   }
