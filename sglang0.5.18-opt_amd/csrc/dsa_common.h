@@ -119,6 +119,22 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 // NaN-quieting max per element.
 __device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 
+// Reduce-scatter of four per-lane values over the four 16-lane rows of the wave: lane l ends
+// with sum over the rows g of v[l / 16] from lane (l % 16) + 16 g, i.e. row g keeps entry g
+// summed over all rows.  Two row-pair exchanges (v_permlane16_swap, each moving a register's odd
+// rows against another's even rows) halve the entries, one half exchange (v_permlane32_swap)
+// halves them again: 3 swaps and 3 adds instead of 4 x (2 swaps + 2 adds) and a select per
+// entry.  The additions associate as ((row 0 + row 1) + (row 2 + row 3)), the order of
+// sum_lanes_16_32, so the results are the same bits.
+__device__ __forceinline__ float reduce_scatter_rows(const float (&v)[4]) {
+  const auto p01 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[0]), __float_as_uint(v[1]), false, false);
+  const auto p23 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[2]), __float_as_uint(v[3]), false, false);
+  const float a = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);  // entry g & 1, rows g, g ^ 1
+  const float b = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);  // entry 2 + (g & 1)
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // x + x[lane ^ 16] and then + x[lane ^ 32], in every lane, with the gfx950 row-swap VALU ops
 // (v_permlane16_swap / v_permlane32_swap) instead of LDS-routed shuffles.  Swapping a register
 // with itself leaves lane l of the two results holding x[l] and x[l ^ 16] (resp. ^ 32), in an

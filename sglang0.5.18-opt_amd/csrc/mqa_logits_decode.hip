@@ -13,8 +13,9 @@
 //    same byte mapping, so the instruction's K ordering is the same permutation on both sides
 //    and cancels.
 //  * Result lane l holds heads 4*(l/16)+i of token l%16: the epilogue is an in-lane
-//    max/fma chain over H/4 values, a row-swap sum over lanes l^16 and l^32, and a lane select
-//    that leaves lane l with token l of the page.  One 256 B logits store per page and row.
+//    max/fma chain over H/4 values; the four sub-tiles' partial sums then go through one
+//    reduce-scatter over the 16-lane rows (row swaps) that leaves lane l with token l of the
+//    page.  One 256 B logits store per page and row.
 //  * K pages go HBM -> LDS by DMA (global_load_lds_dwordx4: no VGPR staging, so register
 //    pressure does not limit the loads in flight).  A CTA runs S page streams; a stream's R
 //    waves (one per row of the group) share each page through an LDS slot, and while a page is
@@ -379,7 +380,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
       dma_page<R>(a.kv + static_cast<int64_t>(s_bt[i + (NS - 1) * S]) * a.page_stride, nxt, r, lane);
     if (i >= n_local) return;  // stream-uniform (the stream still takes part in the barriers)
     const float scale = reinterpret_cast<const float*>(cur + kPageFp8Bytes)[lane];
-    float val = 0.0f;
+    float part[4];  // this lane's heads' share of tokens st * 16 + lane % 16
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const i32x8 kf = lds_frag(cur, st * 16 + t_lo, p0);
@@ -392,9 +393,9 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum += relu_bits(acc[ht][e]) * wf[ht * 4 + e];
       }
-      sum = sum_lanes_16_32(sum);
-      val = (lane >> 4) == st ? sum : val;
+      part[st] = sum;
     }
+    const float val = reduce_scatter_rows(part);  // token `lane` of the page
     const int p = p_begin + i;
     const float v = val * scale;
     pend_p = p;

@@ -10,8 +10,9 @@
 //    double-buffered LDS tile; rows are padded to 144 B so the 16 lanes reading 16 different
 //    keys at one byte offset fall into different banks;
 //  * per page and row: 4 key sub-tiles x H/16 MFMAs (v_mfma_f32_16x16x128_f8f6f4), then the
-//    epilogue of the decode kernel (max/fma over the lane's heads, row-swap sums over l^16, l^32, lane
-//    select) leaves lane l with key l of the page: one 256 B store per page and row;
+//    epilogue of the decode kernel (max/fma over the lane's heads, one reduce-scatter of the four
+//    sub-tiles over the 16-lane rows) leaves lane l with key l of the page: one 256 B store per
+//    page and row;
 //  * causal skipping: a wave skips a page for a row once the page starts at or past len[row];
 //    the CTA stops after the last page any of its rows needs.
 #include "dsa_common.h"
@@ -139,9 +140,12 @@ __global__ __launch_bounds__(kThreads, 2) void mqa_logits_prefill_kernel(const P
       any |= act[r];
     }
     if (any) {
-      float val[kRowsPerWave];
+      float part[kRowsPerWave][4];  // this lane's heads' share of keys st * 16 + lane % 16
 #pragma unroll
-      for (int r = 0; r < kRowsPerWave; ++r) val[r] = 0.0f;
+      for (int r = 0; r < kRowsPerWave; ++r) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) part[r][st] = 0.0f;
+      }
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const uint8_t* src = &s_k[buf][st * 16 * kLdsRow + frag_off];
@@ -158,8 +162,7 @@ __global__ __launch_bounds__(kThreads, 2) void mqa_logits_prefill_kernel(const P
 #pragma unroll
             for (int i = 0; i < 4; ++i) s += relu_bits(acc[ht][i]) * wf[r][ht * 4 + i];
           }
-          s = sum_lanes_16_32(s);
-          val[r] = (lane >> 4) == st ? s : val[r];
+          part[r][st] = s;
         }
       }
       const float scale = s_scale[buf][lane];
@@ -167,7 +170,8 @@ __global__ __launch_bounds__(kThreads, 2) void mqa_logits_prefill_kernel(const P
 #pragma unroll
       for (int r = 0; r < kRowsPerWave; ++r) {
         const int row = row_base + wave * kRowsPerWave + r;
-        if (act[r] && token < len[r]) a.logits[static_cast<int64_t>(row) * a.logits_stride + token] = val[r] * scale;
+        const float val = reduce_scatter_rows(part[r]);  // key `token` of the page
+        if (act[r] && token < len[r]) a.logits[static_cast<int64_t>(row) * a.logits_stride + token] = val * scale;
       }
     }
     if (more) lstore(buf ^ 1, x0, x1, sc);
