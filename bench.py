@@ -375,8 +375,9 @@ def main(argv=None):
         k_ms = kernel_time_ms(step.logits_only, torch)
         kf = step.logits_flops()
         achieved = kf / (k_ms / 1e3) / 1e12
-        traffic, tsrc = profiled_traffic("mqa_logits_prefill_kernel", args.workload)
-        roofline = {"bound": "mfma", "kernel": "mqa_logits_prefill_kernel", "achieved": round(achieved, 1),
+        # prefill runs the paged logits kernel with 8 query rows per CTA
+        traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", args.workload)
+        roofline = {"bound": "mfma", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
                     "traffic": traffic, "traffic_source": tsrc, "algorithmic_flops": kf, "kernel_us": round(k_ms * 1e3, 2)}
         pf = step.path_flops()

@@ -97,7 +97,7 @@ int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* s
  * block_table [B, bt_pages] i32 with row stride bt_stride, width == bt_pages * 64 (mqa_hist.cu:346),
  * logits [B, width] f32 with row stride logits_stride; entries t >= len[r] are not written.
  * mask [B, width / 16] i16 with row stride mask_stride: every word is written.
- * heads in {32, 64}; B % group_size == 0; rows_per_cta divides group_size and is in {1,2,3,4}.
+ * heads in {32, 64}; B % group_size == 0; rows_per_cta divides group_size and is in {1,2,3,4,8}.
  * target_ctas: number of CTAs the K pages are spread over, each CTA streaming a slice of one
  * request (<= 0: as many as are resident at once); the grid is target_ctas + B / rows_per_cta.
  * hist_ws (nullable, int32 [B * (2 * 4096 + 2)], 16-B aligned): the pass-1 workspace of a
@@ -122,7 +122,8 @@ int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t 
  * where key t lives at slot block_table[t / 64] * 64 + t % 64 of kv_cache.  len [rows] i32
  * (causal: prefix + i + 1), clamped to width.  Entries t >= len[r] are not written.
  * q8 [rows, heads, 128] u8; w [rows, heads] f32; block_table [>= ceil(width / 64)] i32;
- * logits [rows, width] f32 with row stride logits_stride. */
+ * logits [rows, width] f32 with row stride logits_stride.  Runs the decode kernel above with the
+ * rows as one group, 8 rows per CTA. */
 int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int heads, int64_t rows,
                            const uint8_t* kv_cache, int64_t page_stride_bytes,
                            const int32_t* block_table, int64_t bt_pages, const int32_t* lens,

@@ -1,4 +1,4 @@
-// Paged MQA indexer logits for decode on gfx950 fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4).
+// Paged MQA indexer logits for decode and prefill on gfx950 fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4).
 //
 //   logits[r, t] = scale[t] * sum_h w[r, h] * relu(q8[r, h, :] . k8[t, :])
 //   mask[r, t/16] bit t%16 = t < len[r] && bits(logits[r, t]) != 0
@@ -32,6 +32,9 @@
 //    hipGraph, and T is chosen so that every CTA is resident at once.
 //  * Mask words past a group's pages are zeroed by the group's own CTAs (a share each, 8-B
 //    stores), so no separate mask memset is launched; a group with no pages still gets a CTA.
+//  * Prefill is the same kernel with a request's query rows as one group in CTAs of 8 rows:
+//    8 waves share one page stream, so a K page is read from HBM once per 8 query rows and
+//    ds_read once per wave; no mask is written (mask == nullptr).
 //  * kHist: also the top-k pass-1 histogram (12-bit key[31:20] of the nonzero logits of rows
 //    with min(hist_len, width) > 2048, plus positive / zero counts), as 16-bit LDS counts (two
 //    bins a word; a CTA's tokens per row stay below 2^16) flushed once per CTA with one global
@@ -319,7 +322,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     const int u0 = static_cast<int>(static_cast<int64_t>(units) * jc / nj);
     const int u1 = static_cast<int>(static_cast<int64_t>(units) * (jc + 1) / nj);
     const bool wide = (reinterpret_cast<uintptr_t>(a.mask) & 7u) == 0 && (a.mask_stride & 3) == 0;
-    for (int u = u0 + tid; u < u1; u += NT) {
+    for (int u = a.mask != nullptr ? u0 + tid : u1; u < u1; u += NT) {
       const int rr = u / tail;
       int16_t* m = a.mask + static_cast<int64_t>(row0 + rr) * a.mask_stride + (pages + u - rr * tail) * 4;
       if (wide) {
@@ -346,7 +349,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   auto flush = [&]() {
     if (pend_p < 0) return;
     const int token = pend_p * kPage + lane;
-    if (lane < 4)
+    if (a.mask != nullptr && lane < 4)
       a.mask[static_cast<int64_t>(row) * a.mask_stride + pend_p * 4 + lane] =
           static_cast<int16_t>((pend_bits >> (16 * lane)) & 0xFFFFu);
     if (token < len) a.logits[static_cast<int64_t>(row) * a.logits_stride + token] = pend_v;
@@ -484,23 +487,71 @@ void launch_r(const DecodeArgs& a, int R, uint32_t grid, hipStream_t stream) {
     case 1: launch_one<H, 1, kHist>(a, grid, stream); break;
     case 2: launch_one<H, 2, kHist>(a, grid, stream); break;
     case 3: launch_one<H, 3, kHist>(a, grid, stream); break;
-    default:
+    case 4:
       if constexpr (!kHist) launch_one<H, 4, false>(a, grid, stream);
+      break;
+    default:
+      if constexpr (!kHist) launch_one<H, 8, false>(a, grid, stream);
       break;
   }
 }
 
 // (CTAs per CU, pages per CTA) of a launch shape, on the host.
 void shape_host(int R, bool hist, int& ctas_per_cu, int& max_pages) {
-  switch (hist ? R + 4 : R) {
+  switch (hist ? R + 16 : R) {
     case 1: ctas_per_cu = Shape<1, false>::kCtasPerCu; max_pages = Shape<1, false>::kMaxPages; break;
     case 2: ctas_per_cu = Shape<2, false>::kCtasPerCu; max_pages = Shape<2, false>::kMaxPages; break;
     case 3: ctas_per_cu = Shape<3, false>::kCtasPerCu; max_pages = Shape<3, false>::kMaxPages; break;
     case 4: ctas_per_cu = Shape<4, false>::kCtasPerCu; max_pages = Shape<4, false>::kMaxPages; break;
-    case 5: ctas_per_cu = Shape<1, true>::kCtasPerCu; max_pages = Shape<1, true>::kMaxPages; break;
-    case 6: ctas_per_cu = Shape<2, true>::kCtasPerCu; max_pages = Shape<2, true>::kMaxPages; break;
+    case 8: ctas_per_cu = Shape<8, false>::kCtasPerCu; max_pages = Shape<8, false>::kMaxPages; break;
+    case 17: ctas_per_cu = Shape<1, true>::kCtasPerCu; max_pages = Shape<1, true>::kMaxPages; break;
+    case 18: ctas_per_cu = Shape<2, true>::kCtasPerCu; max_pages = Shape<2, true>::kMaxPages; break;
     default: ctas_per_cu = Shape<3, true>::kCtasPerCu; max_pages = Shape<3, true>::kMaxPages; break;
   }
+}
+
+// Enqueues the kernel for a.batch rows in groups of R (a.group rows share a block-table row;
+// a.width caps the lengths).  a's pointers, strides and sizes are set and checked by the caller.
+int enqueue(DecodeArgs a, int heads, int R, int target_ctas, bool hist, const int32_t* hist_lens, int32_t* hist_ws,
+            hipStream_t stream, const char* who) {
+  const int64_t n_groups = a.batch / R;
+  DSA_REQUIRE(n_groups <= 0x3FFFFFFF, "%s: too many rows", who);
+  int ctas_per_cu = 1, max_cta_pages = 1;
+  shape_host(R, hist, ctas_per_cu, max_cta_pages);
+  if (target_ctas <= 0) {
+    // All CTAs resident at once: the per-group rounding adds up to one CTA per group, so aim
+    // below the resident count by the group count.
+    int n_cu = 0;
+    const int st = dsa_device_cu_count(&n_cu);
+    if (st != DSA_OK) return st;
+    const int64_t slots = ctas_per_cu * static_cast<int64_t>(n_cu);
+    target_ctas = static_cast<int>(slots - n_groups > slots / 2 ? slots - n_groups : slots / 2);
+  }
+  // Keep every CTA's page slice within the LDS block-table stage: P / T <= max_pages.
+  const int64_t max_pages = n_groups * ((a.width + kPage - 1) / kPage);
+  int64_t target = target_ctas;
+  if (target * max_cta_pages < max_pages) target = (max_pages + max_cta_pages - 1) / max_cta_pages;
+  const int64_t grid = target + n_groups;
+  DSA_REQUIRE(grid <= 0x7FFFFFFF, "%s: grid too large", who);
+  a.R = R;
+  a.n_groups = static_cast<int>(n_groups);
+  a.target = static_cast<int>(target);
+  a.hist_lens = hist ? hist_lens : nullptr;
+  a.hist_ws = hist ? hist_ws : nullptr;
+  a.zero_ws = hist ? nullptr : hist_ws;
+  if (hist) {
+    hipLaunchKernelGGL(mqa_hist_init_kernel, dim3(static_cast<uint32_t>(a.batch)), dim3(256), 0, stream, hist_lens,
+                       a.width, a.batch, hist_ws);
+  }
+  const uint32_t g = static_cast<uint32_t>(grid);
+  if (heads == 64) {
+    if (hist) launch_r<64, true>(a, R, g, stream);
+    else launch_r<64, false>(a, R, g, stream);
+  } else {
+    if (hist) launch_r<32, true>(a, R, g, stream);
+    else launch_r<32, false>(a, R, g, stream);
+  }
+  return check_launch(who);
 }
 
 }  // namespace
@@ -519,8 +570,8 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   DSA_REQUIRE(batch >= 0 && group_size >= 1, "dsa_mqa_logits_decode: batch must be >= 0 and group_size >= 1");
   DSA_REQUIRE(batch % group_size == 0, "dsa_mqa_logits_decode: batch must be a multiple of group_size");
   if (rows_per_cta <= 0) rows_per_cta = group_size % 2 == 0 ? 2 : 1;
-  DSA_REQUIRE(rows_per_cta >= 1 && rows_per_cta <= 4 && group_size % rows_per_cta == 0,
-              "dsa_mqa_logits_decode: rows_per_cta must be in 1..4 and divide group_size");
+  DSA_REQUIRE((rows_per_cta >= 1 && rows_per_cta <= 4 || rows_per_cta == 8) && group_size % rows_per_cta == 0,
+              "dsa_mqa_logits_decode: rows_per_cta must be 1, 2, 3, 4 or 8 and divide group_size");
   DSA_REQUIRE(bt_pages > 0 && bt_pages * kPage <= 0x7FFFFFFF,
               "dsa_mqa_logits_decode: block table capacity must be positive and below 2^31 tokens");
   if (batch == 0) return ok();
@@ -540,27 +591,8 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   const bool hist = fuse_pass1 != 0;
   DSA_REQUIRE(!hist || rows_per_cta <= 3,
               "dsa_mqa_logits_decode: the fused histogram needs rows_per_cta <= 3 (8 KB of LDS per row)");
-  const int64_t n_groups = batch / rows_per_cta;
-  DSA_REQUIRE(n_groups <= 0x3FFFFFFF, "dsa_mqa_logits_decode: batch too large");
-  int ctas_per_cu = 1, max_cta_pages = 1;
-  shape_host(rows_per_cta, hist, ctas_per_cu, max_cta_pages);
-  if (target_ctas <= 0) {
-    // All CTAs resident at once: the per-group rounding adds up to one CTA per group, so aim
-    // below the resident count by the group count.
-    int n_cu = 0;
-    const int st = dsa_device_cu_count(&n_cu);
-    if (st != DSA_OK) return st;
-    const int64_t slots = ctas_per_cu * static_cast<int64_t>(n_cu);
-    target_ctas = static_cast<int>(slots - n_groups > slots / 2 ? slots - n_groups : slots / 2);
-  }
-  // Keep every CTA's page slice within the LDS block-table stage: P / T <= max_pages.
-  const int64_t max_pages = n_groups * bt_pages;
-  int64_t target = target_ctas;
-  if (target * max_cta_pages < max_pages) target = (max_pages + max_cta_pages - 1) / max_cta_pages;
-  const int64_t grid = target + n_groups;
-  DSA_REQUIRE(grid <= 0x7FFFFFFF, "dsa_mqa_logits_decode: grid too large");
 
-  DecodeArgs a;
+  DecodeArgs a{};
   a.q8 = q8;
   a.w = w;
   a.kv = kv_cache;
@@ -575,25 +607,51 @@ extern "C" int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int head
   a.mask = mask;
   a.mask_stride = mask_stride;
   a.group = group_size;
-  a.R = rows_per_cta;
-  a.n_groups = static_cast<int>(n_groups);
-  a.target = static_cast<int>(target);
-  a.hist_lens = hist ? hist_lens : nullptr;
-  a.hist_ws = hist ? hist_ws : nullptr;
-  a.zero_ws = hist ? nullptr : hist_ws;
   a.batch = batch;
+  return enqueue(a, heads, rows_per_cta, target_ctas, hist, hist_lens, hist_ws, stream, "dsa_mqa_logits_decode");
+}
 
-  if (hist) {
-    hipLaunchKernelGGL(mqa_hist_init_kernel, dim3(static_cast<uint32_t>(batch)), dim3(256), 0, stream, hist_lens,
-                       a.width, batch, hist_ws);
+// Prefill: the rows of one request are one group sharing the request's block table, scored by
+// the same kernel in CTAs of 8 rows (8 waves on one LDS page stream: each K page read from HBM
+// once per 8 query rows); a row count that is not a multiple of 8 ends in groups of 4 and of
+// 1-3 rows, each its own launch.  No mask is written.
+extern "C" int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int heads, int64_t rows,
+                                      const uint8_t* kv_cache, int64_t page_stride_bytes, const int32_t* block_table,
+                                      int64_t bt_pages, const int32_t* lens, float* logits, int64_t logits_stride,
+                                      int64_t width, hipStream_t stream) {
+  DSA_REQUIRE(heads == 32 || heads == 64, "dsa_mqa_logits_prefill: heads must be 32 or 64 (got %d)", heads);
+  DSA_REQUIRE(rows >= 0 && rows <= 0x7FFFFFFF, "dsa_mqa_logits_prefill: rows out of range");
+  if (rows == 0) return ok();
+  DSA_REQUIRE(q8 && w && kv_cache && block_table && lens && logits, "dsa_mqa_logits_prefill: null pointer");
+  DSA_REQUIRE(bt_pages > 0 && width > 0 && width <= bt_pages * kPage && width <= 0x7FFFFFFF,
+              "dsa_mqa_logits_prefill: width must be positive and within the block table capacity");
+  DSA_REQUIRE(logits_stride >= width, "dsa_mqa_logits_prefill: logits_stride < width");
+  DSA_REQUIRE(page_stride_bytes >= kPageBytes && page_stride_bytes % 16 == 0 &&
+                  (reinterpret_cast<uintptr_t>(kv_cache) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q8) & 15u) == 0,
+              "dsa_mqa_logits_prefill: kv_cache pages (stride >= 8448, %% 16) and q8 must be 16-B aligned");
+  int64_t done = 0;
+  for (const int R : {8, 4, 2, 1}) {
+    const int64_t n = (rows - done) / R * R;
+    if (n == 0) continue;
+    DecodeArgs a{};
+    a.q8 = q8 + done * heads * kHeadDim;
+    a.w = w + done * heads;
+    a.kv = kv_cache;
+    a.page_stride = page_stride_bytes;
+    a.ctx = lens + done;
+    a.bt = block_table;
+    a.bt_stride = bt_pages;
+    a.bt_pages = static_cast<int>(bt_pages);
+    a.width = static_cast<int>(width);
+    a.logits = logits + done * logits_stride;
+    a.logits_stride = logits_stride;
+    a.mask = nullptr;
+    a.mask_stride = 0;
+    a.group = static_cast<int>(n);
+    a.batch = n;
+    const int st = enqueue(a, heads, R, 0, false, nullptr, nullptr, stream, "dsa_mqa_logits_prefill");
+    if (st != DSA_OK) return st;
+    done += n;
   }
-  const uint32_t g = static_cast<uint32_t>(grid);
-  if (heads == 64) {
-    if (hist) launch_r<64, true>(a, rows_per_cta, g, stream);
-    else launch_r<64, false>(a, rows_per_cta, g, stream);
-  } else {
-    if (hist) launch_r<32, true>(a, rows_per_cta, g, stream);
-    else launch_r<32, false>(a, rows_per_cta, g, stream);
-  }
-  return check_launch("dsa_mqa_logits_decode");
+  return ok();
 }

@@ -44,6 +44,7 @@ def _check_decode(case, lg, mask):
     (6, [2500, 900], 2),
     (6, [2500, 900], 3),
     (4, [1000, 1200], 4),
+    (8, [3000, 70], 8),
 ])
 def test_decode_logits(gpu, heads, group, lens, rpc):
     case = wl.decode_case(100 + len(lens) + group, lens, group=group, heads=heads,
@@ -113,7 +114,9 @@ def test_decode_pass1_workspace_zeroed(gpu, monkeypatch, group, lens):
     _check_decode(case, lg, mask)
 
 
-@pytest.mark.parametrize("heads,n_q,prefix", [(64, 40, 3000), (32, 9, 130), (64, 17, 0)])
+# row counts cover every launch split of the prefill entry: groups of 8, then of 4 and 1-3 rows
+@pytest.mark.parametrize("heads,n_q,prefix", [(64, 40, 3000), (32, 9, 130), (64, 17, 0), (64, 15, 700),
+                                              (32, 6, 4100), (64, 3, 64)])
 def test_prefill_logits(gpu, heads, n_q, prefix):
     case = wl.prefill_case(21 + n_q, n_q, prefix, heads=heads)
     q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
@@ -126,3 +129,32 @@ def test_prefill_logits(gpu, heads, n_q, prefix):
     for r in range(case.rows):
         L = int(case.lens[r])
         check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
+
+
+def test_prefill_writes_only_below_len(gpu):
+    """Through the C ABI into a NaN-filled buffer wider than `width`: row r gets exactly the
+    entries t < min(len[r], width); lengths include 0, negative and past `width`."""
+    import ctypes
+    import os
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(hcu_ops.__file__), "libdsa_indexer.so"))
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    f = lib.dsa_mqa_logits_prefill
+    f.argtypes = [P, P, I, I64, P, I64, P, I64, P, P, I64, I64, P]
+    lib.dsa_last_error.restype = ctypes.c_char_p
+    case = wl.prefill_case(5, 13, 900, heads=64)
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    width = case.n_keys - 37
+    lens = case.lens.clone()
+    lens[0], lens[5], lens[12] = 0, -3, width + 500
+    kv, bt, lens_d = case.kv.to(gpu), case.block_table.to(gpu), lens.to(gpu)
+    out = torch.full((case.rows, width + 19), float("nan"), device=gpu)
+    st = f(q8.data_ptr(), w.data_ptr(), 64, case.rows, kv.data_ptr(), kv.stride(0), bt.data_ptr(), bt.numel(),
+           lens_d.data_ptr(), out.data_ptr(), out.stride(0), width, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.dsa_last_error()
+    got = out.cpu().numpy()
+    ref = hcu_ops.mqa_logits_prefill(q8, w, kv, bt, lens_d, width).cpu().numpy()
+    for r in range(case.rows):
+        L = max(0, min(int(lens[r]), width))
+        assert not np.isnan(got[r, :L]).any(), f"row {r}: entries below len not written"
+        assert np.isnan(got[r, L:]).all(), f"row {r}: entries at or past min(len, width) written"
+        assert np.array_equal(got[r, :L], ref[r, :L]), f"row {r}: differs from the torch binding"
