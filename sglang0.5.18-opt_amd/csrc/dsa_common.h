@@ -84,6 +84,21 @@ __device__ __forceinline__ int wave_sum(int x) {
   return x;
 }
 
+// Inclusive suffix sum over the wave (lane l: sum of lanes l..63).  Within each 16-lane row a
+// Hillis-Steele scan on DPP row shifts (row_shl n: lane l reads lane l + n of its row, 0 past
+// the row's end), then the totals of the rows above, read from their first lanes.
+__device__ __forceinline__ int wave_suffix_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x101, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x102, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x108, 0xF, 0xF, true);
+  const int r1 = __builtin_amdgcn_readlane(x, 16);
+  const int r2 = __builtin_amdgcn_readlane(x, 32);
+  const int r3 = __builtin_amdgcn_readlane(x, 48);
+  const int row = lane_id() >> 4;
+  return x + (row < 1 ? r1 : 0) + (row < 2 ? r2 : 0) + (row < 3 ? r3 : 0);
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -113,6 +128,20 @@ __device__ __forceinline__ int wave_prefix_5(int c, int& total) {
 }
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Slot of this lane among the active lanes of its wave with `pred` set, from one atomic add of
+// their count on *ctr (LDS or global) by the lowest of them.  Lanes without pred get a value
+// they must not use.  Replaces one same-address atomic per lane, which the LDS serialises.
+__device__ __forceinline__ int wave_slot(bool pred, int* ctr) {
+  const uint64_t m = __ballot(pred);
+  int base = 0;
+  if (m != 0) {  // wave-uniform
+    const int leader = static_cast<int>(__builtin_ctzll(m));
+    if (lane_id() == leader) base = atomicAdd(ctr, static_cast<int>(__popcll(m)));
+    base = __builtin_amdgcn_readlane(base, leader);
+  }
+  return base + lanes_below(m);
+}
 
 // max(x, +0) as one integer max on the float bits: negative floats (and -0.0) are negative
 // integers, so they become +0; other values, NaNs included, pass unchanged.  fmaxf would add a

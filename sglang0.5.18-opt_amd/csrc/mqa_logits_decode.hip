@@ -245,9 +245,12 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     }
   }
 
-  if (a.zero_ws != nullptr) {
-    // the top-k's pass-1 workspace [histograms rows*4096 | counters rows*4096 | counts rows*2],
-    // a share per CTA: the histograms in 16-B stores, counter words 0..2 and the counts per row
+  // The top-k's pass-1 workspace [histograms rows*4096 | counters rows*4096 | counts rows*2],
+  // a share per CTA: the histograms in 16-B stores, counter words 0..2 and the counts per row.
+  // Issued after the CTA's page stream: in the prologue the first DMA wait (vmcnt counts
+  // stores too) would wait for these stores as well.
+  auto zero_share = [&]() {
+    if (a.zero_ws == nullptr) return;
     const int64_t units = a.batch * (kBins / 4);
     const int64_t u0 = units * cta / gridDim.x;
     const int64_t u1 = units * (cta + 1) / gridDim.x;
@@ -257,10 +260,13 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
       if (tid < 3) a.zero_ws[(a.batch + rr) * kBins + tid] = 0;
       if (tid < 2) a.zero_ws[2 * a.batch * kBins + 2 * rr + tid] = 0;
     }
-  }
+  };
   __syncthreads();
   const int grp = s_assign[0];
-  if (grp < 0) return;  // uniform: no pages for this CTA
+  if (grp < 0) {  // uniform: no pages for this CTA
+    zero_share();
+    return;
+  }
   const int jc = s_assign[1];
   const int nj = s_assign[2];
 
@@ -420,6 +426,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     }
   }
   flush();
+  zero_share();
 
   if constexpr (kHist) {
     const int n = wave_sum(nz);

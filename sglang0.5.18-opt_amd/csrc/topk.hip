@@ -5,23 +5,26 @@
 // rows with len <= 2048 copy page_table[0:len] and pad with -1.  Only the set is the contract
 // (the order within a row is unspecified here, as it differs between the reference's variants).
 //
-// Algorithm (this file's own; radix digits 12/12/8 of the 32-bit key):
+// Algorithm (this file's own).  Default path, one read of the row: a fixed sample of the row
+// (256 chunks of 16 tokens, or the whole row up to 4096 tokens) gives a key K* that leaves, with
+// overwhelming probability, between 2048 and a few thousand of the row's keys >= K*; one
+// unordered pass collects them (positions from wave-aggregated LDS atomics, no barriers in the
+// streaming loop); they are resolved exactly by a 12-bit histogram of a digit relative to K*
+// (sized from the sample so that the threshold digit holds a handful of keys) and an exact
+// (key desc, token asc) rank of that digit's members.  If the count misses [2048, capacity] the
+// row takes the exact path, so the result never depends on the sample.
+// Exact path (radix digits 12/12/8 of the 32-bit key):
 //   pass 1   histogram of key[31:20] over the nonzero tokens plus positive / zero counts (or
 //            taken from the logits kernel).  positives <= 2048 <= positives + zeros means the
 //            threshold is +0 (sparse fast path).  Otherwise the threshold digit t1 follows.
 //   collect  one unordered pass over the row: tokens above bin t1 (or positive, fast path) are
-//            written straight to the output, tokens in bin t1 become candidates (key, token);
-//            positions come from wave-aggregated LDS atomics, so the streaming loop has no
-//            barriers and keeps several loads in flight per lane.
-//   resolve  the candidates (in LDS) go through the three digit passes to the exact threshold
-//            key and the number `remaining` of threshold ties to take.  If there are more ties
-//            than that, a second radix select over ~token among the ties keeps the lowest
-//            indices.  Fast path: the first `remaining` zeros come from an ordered scan of the
-//            row's prefix, which stops as soon as enough were found.
+//            written straight to the output, tokens in bin t1 become candidates (key, token).
+//   resolve  the candidates (in LDS) go through the remaining digit passes to the exact
+//            threshold key and the number of threshold ties to take (the lowest indices).  Fast
+//            path: the first zeros come from an ordered scan of the row's prefix.
 //   overflow candidates that do not fit in LDS are resolved by re-reading the row.
-// Few rows: S CTAs per row collect one slice each (taking pass 1 from the logits kernel, or
-// from a split pass-1 kernel), publish their A tokens and candidates through per-row global
-// counters, and the last CTA of the row to finish (device-scope atomic) resolves the threshold.
+// Few rows: S CTAs per row collect one slice each and publish their candidates through per-row
+// global counters; the last CTA of the row to finish (device-scope atomic) resolves them.
 // Many rows: one CTA per row does everything.  No host synchronisation; launch shapes depend
 // only on (rows, width, splits), so the whole path can be captured in a hipGraph.
 #include "dsa_common.h"
@@ -122,30 +125,21 @@ __device__ __forceinline__ int block_prefix(int c, int& total, int* s_scan, int 
   return before + x;
 }
 
-// Finds bin t with suffix(t) >= need > suffix(t + 1) of a histogram held in registers (thread
-// tid owns bins tid * BPT .. tid * BPT + BPT - 1); s_res = {t, suffix(t + 1), count of t} ({0, 0,
-// 0} if the histogram holds fewer than `need`, which consistent inputs never do).  Ends with a
-// barrier.
-template <int NT, int BPT>
-__device__ void find_threshold_regs(const int (&h)[BPT], int need, int* s_wtot, int* s_res) {
+// Finds, for each need[i], bin t with suffix(t) >= need[i] > suffix(t + 1) of a histogram held
+// in registers (thread tid owns bins tid * BPT .. tid * BPT + BPT - 1); s_res[3i..3i+2] = {t,
+// suffix(t + 1), count of t} ({0, 0, 0} if the histogram holds fewer than need[i], which
+// consistent inputs never do).  Ends with a barrier.
+template <int NT, int BPT, int NN>
+__device__ void find_thresholds_regs(const int (&h)[BPT], const int (&need)[NN], int* s_wtot, int* s_res) {
   constexpr int W = NT / kWave;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  if (tid == 0) {
-    s_res[0] = 0;
-    s_res[1] = 0;
-    s_res[2] = 0;
-  }
+  if (tid < 3 * NN) s_res[tid] = 0;
   int s = 0;
 #pragma unroll
   for (int j = 0; j < BPT; ++j) s += h[j];
-  int x = s;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_down(x, o);
-    if (lane + o < kWave) x += y;
-  }
+  const int x = wave_suffix_sum(s);
   if (lane == 0) s_wtot[w] = x;
   __syncthreads();
   int after = 0;
@@ -153,31 +147,46 @@ __device__ void find_threshold_regs(const int (&h)[BPT], int need, int* s_wtot, 
   for (int v = 0; v < W; ++v) after += v > w ? s_wtot[v] : 0;
   const int suf = x + after;
   const int suf_next = suf - s;
-  if (suf >= need && suf_next < need) {
-    int acc = suf_next;
 #pragma unroll
-    for (int j = BPT - 1; j >= 0; --j) {
-      if (acc + h[j] >= need) {
-        s_res[0] = tid * BPT + j;
-        s_res[1] = acc;
-        s_res[2] = h[j];
-        break;
+  for (int i = 0; i < NN; ++i) {
+    if (suf >= need[i] && suf_next < need[i]) {
+      int acc = suf_next;
+#pragma unroll
+      for (int j = BPT - 1; j >= 0; --j) {
+        if (acc + h[j] >= need[i]) {
+          s_res[3 * i] = tid * BPT + j;
+          s_res[3 * i + 1] = acc;
+          s_res[3 * i + 2] = h[j];
+          break;
+        }
+        acc += h[j];
       }
-      acc += h[j];
     }
   }
   __syncthreads();
 }
 
+template <int NT, int BPT>
+__device__ void find_threshold_regs(const int (&h)[BPT], int need, int* s_wtot, int* s_res) {
+  const int n[1] = {need};
+  find_thresholds_regs<NT, BPT, 1>(h, n, s_wtot, s_res);
+}
+
 // The same over an LDS histogram of NB bins.
-template <int NB, int NT>
-__device__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_res) {
+template <int NB, int NT, int NN>
+__device__ void find_thresholds(const int* hist, const int (&need)[NN], int* s_wtot, int* s_res) {
   constexpr int BPT = NB >= NT ? NB / NT : 1;
   constexpr int ACTIVE = NB / BPT;
   int h[BPT];
 #pragma unroll
   for (int j = 0; j < BPT; ++j) h[j] = static_cast<int>(threadIdx.x) < ACTIVE ? hist[threadIdx.x * BPT + j] : 0;
-  find_threshold_regs<NT, BPT>(h, need, s_wtot, s_res);
+  find_thresholds_regs<NT, BPT, NN>(h, need, s_wtot, s_res);
+}
+
+template <int NB, int NT>
+__device__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_res) {
+  const int n[1] = {need};
+  find_thresholds<NB, NT, 1>(hist, n, s_wtot, s_res);
 }
 
 template <int NT>
@@ -371,6 +380,207 @@ __device__ void collect(const RowSrc& rr, int b, int n_batches, const Meta& m, c
                            [&](int bb, const Batch& x) { process_batch<NT>(rr, bb, x, m, st); });
 }
 
+// ---------------------------------------------------------------------------------------------
+// Sampled threshold.  A row of len > 2048 tokens is read once: every key >= K* is collected,
+// where K* is a key of a fixed sample of the row chosen so that, with overwhelming probability
+// for any ordering of the values, at least 2048 and at most a few thousand keys of the row are
+// >= K*.  The top-2048 then lies among the collected keys (every other key is < K*) and is
+// resolved exactly among them; when the count misses that window the row takes the exact
+// two-pass path instead, so the result never depends on the sample.
+//
+// Sample: 256 chunks of 16 aligned tokens spread evenly over the row (one 64-B sector of
+// scores and one mask word each), or the whole row when it has <= 4096 tokens.  K* is the
+// sample key of rank k (descending) with k = mu + 4 sqrt(mu) + 2, mu = 2048 * 4096 / len the
+// expected number of sample keys above the row's 2048th key: the row has fewer than 2048 keys
+// >= K* only if the sample holds >= k keys above the 2048th, a 4-sigma binomial event, and
+// about len * k / 4096 ~ 2048 + 4.5 sqrt(2048 len / 4096) keys are collected.
+constexpr int kSampleChunks = 256;
+constexpr int kSample = kSampleChunks * 16;
+
+__device__ __forceinline__ int sample_rank(int len) {
+  if (len <= kSample) return kTopK;  // the sample is the row: K* is its 2048th key
+  const float mu = static_cast<float>(kTopK) * static_cast<float>(kSample) / static_cast<float>(len);
+  const int k = static_cast<int>(ceilf(mu + 4.0f * sqrtf(mu) + 2.0f));
+  return k < kSample ? k : kSample;
+}
+
+// Rank of the sample key that estimates the row's 2048th key (mu, rounded).
+__device__ __forceinline__ int sample_mid_rank(int len) {
+  if (len <= kSample) return kTopK;
+  const int m = static_cast<int>(static_cast<float>(kTopK) * static_cast<float>(kSample) / static_cast<float>(len) + 0.5f);
+  return m < 1 ? 1 : m;
+}
+
+// First token of sample quad s (4 tokens) of a row.
+__device__ __forceinline__ int sample_quad(int len, int s) {
+  if (len <= kSample) return s * 4;
+  const int c = s >> 2;
+  int start = static_cast<int>((static_cast<int64_t>(2 * c + 1) * len) / (2 * kSampleChunks)) & ~15;
+  const int last = (len - 16) & ~15;
+  start = start < last ? start : last;
+  return start + (s & 3) * 4;
+}
+
+// The collection threshold of a row and the digit its candidates are resolved on:
+// min(4095, (key - thr) >> shift), monotone in the key above thr.  shift is set from the
+// sample so that the span from K* to the estimated 2048th key covers ~1000-2000 digits: the
+// threshold digit then holds a handful of candidates.
+struct SampleCut {
+  uint32_t thr;
+  int shift;
+};
+
+__device__ __forceinline__ uint32_t cand_digit(uint32_t key, const SampleCut& c) {
+  const uint32_t d = (key - c.thr) >> c.shift;
+  return d < 4095u ? d : 4095u;
+}
+
+// Scratch of the threshold search (LDS): a 12-bit histogram and the keys of one bin's members.
+struct SampleLds {
+  int* hist;      // kBins
+  uint32_t* mk;   // NT, 16-B aligned
+  int* wtot;      // NT / kWave
+  int* res;       // 6
+  int* misc;      // 2
+};
+
+// This thread's share of a row's sample, loaded (sample_issue) but not yet used, so that the
+// caller's own loads can follow it into the memory pipeline before the sample is waited for.
+template <int NT>
+struct SampleLoads {
+  static constexpr int QPT = kSample / 4 / NT;  // sample quads per thread
+  static_assert(QPT >= 1 && QPT * 4 * NT == kSample, "sample split over the block");
+  Quad q[QPT];
+  int i0[QPT];
+};
+
+template <bool kVec, int NT>
+__device__ __forceinline__ void sample_issue(const RowSrc& r, SampleLoads<NT>& x) {
+#pragma unroll
+  for (int j = 0; j < SampleLoads<NT>::QPT; ++j) {
+    x.i0[j] = sample_quad(r.len, static_cast<int>(threadIdx.x) + j * NT);
+    load_quad<kVec>(r, x.i0[j], x.q[j]);
+  }
+}
+
+// K* of row r and the candidate digit from its issued sample (block-uniform; every CTA of the
+// row computes the same).
+template <int NT>
+__device__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x, const SampleLds& S) {
+  constexpr int QPT = SampleLoads<NT>::QPT;
+  const int tid = threadIdx.x;
+  const Quad* q = x.q;
+  const int* i0 = x.i0;
+  zero_lds<NT>(S.hist, kBins);
+  if (tid == 0) S.misc[0] = 0;
+  __syncthreads();
+  uint32_t k[QPT][4], v[QPT];
+#pragma unroll
+  for (int j = 0; j < QPT; ++j) {
+    v[j] = quad_keys(r, i0[j], q[j], k[j]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if ((v[j] >> e) & 1u) atomicAdd(&S.hist[k[j][e] >> 20], 1);
+  }
+  __syncthreads();
+  const int rank = sample_rank(r.len);
+  const int needs[2] = {rank, sample_mid_rank(r.len)};
+  find_thresholds<kBins, NT, 2>(S.hist, needs, S.wtot, S.res);
+  const uint32_t b = static_cast<uint32_t>(S.res[0]);
+  const int need = rank - S.res[1];  // rank of K* within bin b, 1 .. count(b)
+  const int cnt = S.res[2];
+  const uint32_t bm = static_cast<uint32_t>(S.res[3]);  // bin of the 2048th-key estimate (>= b)
+  const uint32_t span = bm > b ? bm - b + 1u : 1u;         // <= 4096
+  SampleCut cut;
+  cut.shift = 9 + (32 - __builtin_clz(span));              // 10 .. 22
+  if (cnt > NT) {  // block-uniform; a heavy bin: its lower edge (a superset)
+    cut.thr = b << 20;
+    return cut;
+  }
+  static_assert(QPT * 4 <= 16, "member masks hold 16 keys");
+  uint32_t fm = 0;
+#pragma unroll
+  for (int j = 0; j < QPT; ++j) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) fm |= static_cast<uint32_t>(((v[j] >> e) & 1u) && (k[j][e] >> 20) == b) << (j * 4 + e);
+  }
+  {
+    int tm;
+    int pm = wave_prefix_5(__popc(fm), tm);
+    int base = 0;
+    if (tm != 0 && lane_id() == 0) base = atomicAdd(&S.misc[0], tm);
+    pm += uniform(base);
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if ((fm >> (j * 4 + e)) & 1u) S.mk[pm++] = k[j][e];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < cnt) {
+    const uint32_t x = S.mk[tid];
+    int gt = 0, eq = 0;
+    int i = 0;
+#pragma unroll 4
+    for (; i + 4 <= cnt; i += 4) {  // 16-B LDS reads
+      const uint4 y = *reinterpret_cast<const uint4*>(S.mk + i);
+      gt += (y.x > x) + (y.y > x) + (y.z > x) + (y.w > x);
+      eq += (y.x == x) + (y.y == x) + (y.z == x) + (y.w == x);
+    }
+    for (; i < cnt; ++i) {
+      gt += S.mk[i] > x;
+      eq += S.mk[i] == x;
+    }
+    if (gt < need && need <= gt + eq) S.misc[1] = static_cast<int>(x);
+  }
+  __syncthreads();
+  cut.thr = static_cast<uint32_t>(S.misc[1]);
+  return cut;
+}
+
+// Keys >= thr of a batch into the LDS list (ck, ci) at slots from one wave-aggregated atomic;
+// the count keeps growing past cap (the caller sees the overflow), the stores stop at cap.
+template <int NT>
+__device__ __forceinline__ void process_ge(const RowSrc& rr, int b, const Batch& x, uint32_t thr, uint32_t* ck,
+                                           int* ci, int* n, int cap) {
+  uint32_t k[kUnroll][4];
+  uint32_t f = 0;
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t v = quad_keys(rr, b + u * NT * 4, x.q[u], k[u]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f |= static_cast<uint32_t>(((v >> j) & 1u) && k[u][j] >= thr) << (u * 4 + j);
+  }
+  int t;
+  int p = wave_prefix_5(__popc(f), t);
+  if (t == 0) return;  // wave-uniform
+  int base = 0;
+  if (lane_id() == 0) base = atomicAdd(n, t);
+  p += uniform(base);
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if ((f >> (u * 4 + j)) & 1u) {
+        if (p < cap) {
+          ck[p] = k[u][j];
+          ci[p] = b + u * NT * 4 + j;
+        }
+        ++p;
+      }
+    }
+  }
+}
+
+template <bool kVec, int NT>
+__device__ void collect_ge(const RowSrc& rr, int b, int n_batches, uint32_t thr, uint32_t* ck, int* ci, int* n,
+                           int cap, Batch& x0, Batch& x1) {
+  stream_batches<kVec, NT>(rr, b, n_batches, x0, x1,
+                           [&](int bb, const Batch& x) { process_ge<NT>(rr, bb, x, thr, ck, ci, n, cap); });
+}
+
 // Radix select over LDS members: the key `thr` such that `need` members have key >= thr and the
 // number of members with key > thr (returned in above).  key_of(e) / member(e) index 0..n-1.
 // d1_known >= 0: every member's key[31:20] is d1_known (the first digit pass is skipped).
@@ -426,21 +636,21 @@ struct ResolveLds {
   int scan[2 * (NT / kWave)];
   int wtot[NT / kWave];
   int red[NT / kWave];
-  int res[3];
+  int res[6];
   int misc[4];
 };
 
-// Resolves the LDS candidates (all in bin t1, unordered) of a row whose above1 tokens above
-// bin t1 are already in dst[0, above1): digit passes over key[19:8] and key[7:0], then the
-// ties at the threshold key, lowest tokens first.  The general path of resolve_lds.
+// Resolves the LDS candidates (unordered) of a row whose above1 tokens above them are already in
+// dst[0, above1): radix passes over the key (the first skipped when all share key[31:20] = d1
+// >= 0), then the ties at the threshold key, lowest tokens first.  The general path of
+// resolve_lds and resolve_cands.
 template <int NT, int CAP>
-__device__ void resolve_lds_radix(ResolveLds<NT, CAP>& L, int n_c, uint32_t t1, int above1, const PtRow& pt,
+__device__ void resolve_lds_radix(ResolveLds<NT, CAP>& L, int n_c, int d1, int above1, const PtRow& pt,
                                   int32_t* dst) {
   const int need1 = kTopK - above1;
   int gt;
   const uint32_t thr = radix_select<NT>(
-      n_c, need1, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt,
-      static_cast<int>(t1));
+      n_c, need1, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt, d1);
   const int remaining = need1 - gt;
   const int tie_base = kTopK - remaining;
   // ties at thr: all of them, unless there are more than `remaining` -- then the lowest tokens,
@@ -491,24 +701,27 @@ __device__ void resolve_lds(ResolveLds<NT, CAP>& L, int n_c, uint32_t t1, int ab
   const int above2 = L.res[1];
   const int n2 = L.res[2];
   if (n2 > NT) {  // block-uniform
-    resolve_lds_radix(L, n_c, t1, above1, pt, dst);
+    resolve_lds_radix(L, n_c, static_cast<int>(t1), above1, pt, dst);
     return;
   }
   const int need2 = need1 - above2;  // members to take
   // the histogram is consumed: its first 2 * NT words hold the members' keys and tokens
   uint32_t* mk = reinterpret_cast<uint32_t*>(L.hist);
   int* mt = L.hist + NT;
-  for (int e = threadIdx.x; e < n_c; e += NT) {
-    const uint32_t k = L.ck[e];
+  for (int base = 0; base < n_c; base += NT) {  // block-uniform trip count
+    const int e = base + static_cast<int>(threadIdx.x);
+    const bool in = e < n_c;
+    const uint32_t k = in ? L.ck[e] : 0u;
+    const int tok = in ? L.ci[e] : 0;
     const uint32_t d = (k >> 8) & 0xFFFu;
-    if (d > d2) {
-      put(dst, above1 + atomicAdd(&L.misc[0], 1), pt[L.ci[e]]);
-    } else if (d == d2) {
-      const int q = atomicAdd(&L.misc[1], 1);
-      if (q < NT) {
-        mk[q] = k;
-        mt[q] = L.ci[e];
-      }
+    const bool ga = in && d > d2;
+    const bool gm = in && d == d2;
+    const int sa = wave_slot(ga, &L.misc[0]);
+    const int sm = wave_slot(gm, &L.misc[1]);
+    if (ga) put(dst, above1 + sa, pt[tok]);
+    if (gm && sm < NT) {
+      mk[sm] = k;
+      mt[sm] = tok;
     }
   }
   __syncthreads();
@@ -517,11 +730,105 @@ __device__ void resolve_lds(ResolveLds<NT, CAP>& L, int n_c, uint32_t t1, int ab
     const uint32_t k = mk[t];
     const int tok = mt[t];
     int rank = 0;
-    for (int j = 0; j < n2; ++j) {
-      const uint32_t kj = mk[j];
-      rank += kj > k || (kj == k && mt[j] < tok);
+    int j = 0;
+#pragma unroll 4
+    for (; j + 4 <= n2; j += 4) {  // 16-B LDS reads (mk and mt are 16-B aligned)
+      const uint4 kj = *reinterpret_cast<const uint4*>(mk + j);
+      const int4 tj = *reinterpret_cast<const int4*>(mt + j);
+      rank += (kj.x > k || (kj.x == k && tj.x < tok)) + (kj.y > k || (kj.y == k && tj.y < tok)) +
+              (kj.z > k || (kj.z == k && tj.z < tok)) + (kj.w > k || (kj.w == k && tj.w < tok));
     }
+    for (; j < n2; ++j) rank += mk[j] > k || (mk[j] == k && mt[j] < tok);
     if (rank < need2) put(dst, kTopK - need2 + rank, pt[tok]);
+  }
+}
+
+// Resolves n (kTopK <= n <= CAP) collected candidates (keys >= cut.thr) that hold the row's top
+// 2048; load(e, k, t) fetches candidate e (from LDS, or from the row's published list).  A
+// histogram of their digit cand_digit gives the threshold digit t1: candidates above it go
+// straight to the output, its members are ranked exactly by (key desc, token asc) -- a handful
+// by the choice of the digit -- or, when there are more than NT, resolved by radix passes.
+template <int NT, int CAP, typename Load>
+__device__ void resolve_cands(ResolveLds<NT, CAP>& L, int n, const SampleCut& cut, const PtRow& pt, int32_t* dst,
+                              Load load) {
+  constexpr int EPT = CAP / NT;
+  static_assert(EPT * NT == CAP, "candidates split over the block");
+  const int tid = threadIdx.x;
+  uint32_t kk[EPT];
+  int tt[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {  // every load in flight before the first use
+    const int e = tid + j * NT;
+    kk[j] = 0u;
+    tt[j] = 0;
+    if (e < n) load(e, kk[j], tt[j]);
+  }
+  int32_t pv[EPT];  // page-table entries, fetched while the threshold is searched
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) pv[j] = tid + j * NT < n ? pt[tt[j]] : -1;
+  zero_lds<NT>(L.hist, kBins);
+  if (tid == 0) L.misc[0] = L.misc[1] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (tid + j * NT < n) atomicAdd(&L.hist[cand_digit(kk[j], cut)], 1);
+  __syncthreads();
+  find_threshold<kBins, NT>(L.hist, kTopK, L.wtot, L.res);
+  const uint32_t t1 = static_cast<uint32_t>(L.res[0]);
+  const int above1 = L.res[1];
+  const int n_t1 = L.res[2];
+  const bool direct = n_t1 <= NT;  // block-uniform: members ranked directly, their entries in hist
+  static_assert(EPT <= 16, "masks hold 16 candidates");
+  uint32_t fa = 0, fm = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const bool in = tid + j * NT < n;
+    const uint32_t d = cand_digit(kk[j], cut);
+    fa |= static_cast<uint32_t>(in && d > t1) << j;
+    fm |= static_cast<uint32_t>(in && d == t1) << j;
+  }
+  {
+    int ta, tm;
+    int pa = wave_prefix_5(__popc(fa), ta);
+    int pm = wave_prefix_5(__popc(fm), tm);
+    int ba = 0, bm = 0;
+    if (lane_id() == 0) {
+      if (ta) ba = atomicAdd(&L.misc[0], ta);
+      if (tm) bm = atomicAdd(&L.misc[1], tm);
+    }
+    pa += uniform(ba);
+    pm += uniform(bm);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      if ((fa >> j) & 1u) put(dst, pa++, pv[j]);
+      if ((fm >> j) & 1u) {
+        L.ck[pm] = kk[j];
+        L.ci[pm] = tt[j];
+        if (direct) L.hist[pm] = pv[j];
+        ++pm;
+      }
+    }
+  }
+  __syncthreads();
+  if (!direct) {
+    resolve_lds_radix(L, n_t1, -1, above1, pt, dst);
+    return;
+  }
+  const int need1 = kTopK - above1;
+  if (tid < n_t1) {
+    const uint32_t k = L.ck[tid];
+    const int tok = L.ci[tid];
+    int rank = 0;
+    int j = 0;
+#pragma unroll 4
+    for (; j + 4 <= n_t1; j += 4) {  // 16-B LDS reads (ck and ci are 16-B aligned)
+      const uint4 kj = *reinterpret_cast<const uint4*>(L.ck + j);
+      const int4 tj = *reinterpret_cast<const int4*>(L.ci + j);
+      rank += (kj.x > k || (kj.x == k && tj.x < tok)) + (kj.y > k || (kj.y == k && tj.y < tok)) +
+              (kj.z > k || (kj.z == k && tj.z < tok)) + (kj.w > k || (kj.w == k && tj.w < tok));
+    }
+    for (; j < n_t1; ++j) rank += L.ck[j] > k || (L.ck[j] == k && L.ci[j] < tok);
+    if (rank < need1) put(dst, above1 + rank, L.hist[tid]);
   }
 }
 
@@ -617,7 +924,7 @@ struct TopkArgs {
   const int32_t* cu;
   int n_req;
   int32_t* out;
-  int S;             // slices per row of the split pass-1 kernel
+  int S;             // CTAs per row of the sampled split kernel
   int T;             // CTAs the balanced split kernel spreads the rows' tokens over
   int32_t* ghist;    // [rows][kBins]  pass-1 histogram
   int32_t* gcnt;     // [rows][2] = (positives, zeros)
@@ -655,8 +962,45 @@ __device__ __forceinline__ void copy_short_row(const PtRow& pt, int32_t* dst, in
   for (int i = threadIdx.x; i < kTopK; i += NT) dst[i] = i < len ? pt[i] : -1;
 }
 
+// The exact two-pass selection of one row by one CTA: pass-1 histogram, collection above / in
+// the threshold bin (s_a: kTopK staged tokens above it; at most cap_c candidates in L.ck /
+// L.ci), resolution in LDS or by re-reading the row.  Not inlined: it is the rare path of the
+// sampled kernels, whose register budget it would otherwise set.
+template <bool kVec, int NT, int CAP>
+__device__ __attribute__((noinline)) void exact_row(ResolveLds<NT, CAP>& L, int* s_a, int cap_c, const RowSrc r,
+                                                    const PtRow pt, int32_t* dst) {
+  constexpr int kStep = NT * 4 * kUnroll;
+  int pos, zeros;
+  pass_hist<kVec, NT>(r, 0, r.len, L.hist, L.red, pos, zeros);
+  if (threadIdx.x == 0 && zeros) L.hist[kZeroBin] += zeros;
+  const int b0 = static_cast<int>(threadIdx.x) * 4;
+  Batch x0, x1;
+  load_batch<kVec, NT>(r, b0, x0);
+  load_batch<kVec, NT>(r, b0 + kStep, x1);
+  __syncthreads();
+  const Meta m = row_meta<NT>(L.hist, pos, zeros, L.wtot, L.res);
+  if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
+  __syncthreads();
+  Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, cap_c};
+  collect<kVec, NT>(r, b0, (r.len + kStep - 1) / kStep, m, st, x0, x1);
+  __syncthreads();
+  const int n_a = min(L.misc[0], kTopK);
+  const int n_c = L.misc[1];
+  for (int i = threadIdx.x; i < n_a; i += NT) put(dst, i, pt[s_a[i]]);
+  if (m.fast) {
+    ordered_scan<kVec, NT>(
+        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
+  } else if (n_c <= cap_c) {
+    resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
+  } else {
+    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
-// One CTA per row.  kPre: pass 1 (histogram + counts) comes from a.ghist / a.gcnt.
+// One CTA per row.  kPre: pass 1 (histogram + counts) comes from a.ghist / a.gcnt and the row
+// is collected against its exact threshold bin; otherwise against the sampled threshold K*
+// (one read of the row), with the exact path when the collected count misses [2048, kCapC].
 template <bool kVec, bool kPre>
 __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   __shared__ ResolveLds<kTk, kCapC> L;
@@ -674,7 +1018,6 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   const int b0 = static_cast<int>(threadIdx.x) * 4;
   const int n_batches = (len + kStep - 1) / kStep;
   Batch x0, x1;
-  Meta m;
   if constexpr (kPre) {
     // pass-1 slots (4 bins per thread) first, then the first two batches, so that waiting for
     // the histogram does not wait for the batches
@@ -683,6 +1026,7 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
     const int zeros = a.gcnt[2 * row + 1];
     load_batch<kVec, kTk>(r, b0, x0);
     load_batch<kVec, kTk>(r, b0 + kStep, x1);
+    Meta m;
     m.pos = pos;
     m.fast = pos <= kTopK && pos + zeros >= kTopK;
     m.t1 = 0;
@@ -696,43 +1040,49 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
     } else {
       __syncthreads();
     }
+    Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
+    collect<kVec, kTk>(r, b0, n_batches, m, st, x0, x1);
+    __syncthreads();
+    const int n_a = min(L.misc[0], kTopK);
+    const int n_c = L.misc[1];
+    for (int i = threadIdx.x; i < n_a; i += kTk) put(dst, i, pt[s_a[i]]);
+    if (m.fast) {
+      ordered_scan<kVec, kTk>(
+          r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
+    } else if (n_c <= kCapC) {
+      resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
+    } else {
+      resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
+    }
   } else {
-    int pos, zeros;
-    pass_hist<kVec, kTk>(r, 0, len, L.hist, L.red, pos, zeros);
-    if (threadIdx.x == 0 && zeros) L.hist[kZeroBin] += zeros;
+    SampleLoads<kTk> smp;
+    sample_issue<kVec, kTk>(r, smp);  // the sample first: it is needed first
     load_batch<kVec, kTk>(r, b0, x0);
     load_batch<kVec, kTk>(r, b0 + kStep, x1);
+    const SampleLds S{L.hist, L.ck, L.wtot, L.res, L.misc};
+    const SampleCut cut = sample_threshold<kTk>(r, smp, S);
+    if (threadIdx.x == 0) L.misc[2] = 0;
     __syncthreads();
-    m = row_meta<kTk>(L.hist, pos, zeros, L.wtot, L.res);
-    if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
+    collect_ge<kVec, kTk>(r, b0, n_batches, cut.thr, L.ck, L.ci, &L.misc[2], kCapC, x0, x1);
     __syncthreads();
-  }
-  Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
-  collect<kVec, kTk>(r, b0, n_batches, m, st, x0, x1);
-  __syncthreads();
-  const int n_a = min(L.misc[0], kTopK);
-  const int n_c = L.misc[1];
-  for (int i = threadIdx.x; i < n_a; i += kTk) put(dst, i, pt[s_a[i]]);
-  if (m.fast) {
-    ordered_scan<kVec, kTk>(
-        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
-  } else if (n_c <= kCapC) {
-    resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
-  } else {
-    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
+    const int n = L.misc[2];
+    if (n >= kTopK && n <= kCapC) {  // block-uniform
+      resolve_cands(L, n, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
+        k = L.ck[e];
+        t = L.ci[e];
+      });
+    } else {
+      exact_row<kVec, kTk>(L, s_a, kCapC, r, pt, dst);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Split variant.  CTAs cover balanced slices of the rows (split_assign).
-// Zeroes the pass-1 histogram, counts and per-row counters of the split path.
-__global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ ghist, int32_t* __restrict__ gcnt,
-                                                        int32_t* __restrict__ ctr, int64_t ctr_stride) {
-  const int row = blockIdx.x;
-  int4* g = reinterpret_cast<int4*>(ghist + static_cast<int64_t>(row) * kBins);
-  for (int i = threadIdx.x; i < kBins / 4; i += 256) g[i] = make_int4(0, 0, 0, 0);
-  if (threadIdx.x < 2) gcnt[2 * row + threadIdx.x] = 0;
-  if (threadIdx.x < 3) ctr[row * ctr_stride + threadIdx.x] = 0;
+// Zeroes the per-row counters of the split path (4 words a row).
+__global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ ctr, int rows) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < 4 * rows) ctr[i] = 0;
 }
 
 struct SplitLds {
@@ -745,18 +1095,24 @@ struct SplitLds {
     ResolveLds<kTs, kCapS> res;     // the row's resolution (last CTA only)
   } u;
   int wtot[kTs / kWave];
-  int res[3];
+  int res[6];
   int n[6];
   long long lsum[kTs / kWave];
   int slot[3];
 };
 
-struct HistLds {
-  int hist[kBins];
-  int red[kTs / kWave];
+struct SampledLds {
+  union {
+    struct {
+      uint32_t ck[kCapS];
+      int ci[kCapS];
+    } col;                          // this CTA's keys >= K*
+    ResolveLds<kTs, kCapS> res;     // the threshold search; the row's resolution (last CTA)
+  } u;
   int wtot[kTs / kWave];
-  long long lsum[kTs / kWave];
-  int slot[3];
+  int res[6];
+  int misc[2];
+  int n[4];
 };
 
 // Balanced split: row r gets c_r = ceil(len_r * T / L) CTAs (L = the summed lengths of the rows
@@ -813,35 +1169,84 @@ __device__ __forceinline__ bool split_slice(int len, int c, int j, int& begin, i
 
 // Pass 1 of one balanced slice (the split kernel's slices) into the row's global histogram and
 // positive / zero counts, which start at zero.
+// Split with the sampled threshold: CTA c takes slice c % S of row c / S (S CTAs a row, the
+// whole grid resident), so it starts loading without a length-dependent assignment.  Every
+// CTA of a row computes the same K* from the row's sample, collects its slice's keys >= K* and
+// publishes them (device-coherent stores at slots from the row's counter); the last CTA of the
+// row resolves them, or runs the exact path over the row when their count missed [2048, kCapS].
+// Counters (zero on entry): [1] keys published, [2] CTAs done.
 template <bool kVec>
-__global__ __launch_bounds__(kTs) void topk_split_hist_kernel(const TopkArgs a) {
-  __shared__ HistLds L;
-  split_assign(a, a.T, L);
-  const int row = L.slot[0];
-  if (row < 0) return;  // block-uniform
+__global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void topk_split_sampled_kernel(const TopkArgs a) {
+  __shared__ SampledLds L;
+  constexpr int kStep = kTs * 4 * kUnroll;
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x / a.S;
+  const int slice = blockIdx.x - row * a.S;
   const int len = row_len(a, row);
-  if (len <= kTopK) return;
-  int begin, end, n_sl;
-  if (!split_slice(len, L.slot[2], L.slot[1], begin, end, n_sl)) return;
-  int pos, zeros;
-  pass_hist<kVec, kTs>(row_src(a, row, len), begin, end, L.hist, L.red, pos, zeros);
-  int32_t* gh = a.ghist + static_cast<int64_t>(row) * kBins;
-  for (int i = threadIdx.x; i < kBins; i += kTs) {
-    const int c = L.hist[i] + (i == kZeroBin ? zeros : 0);
-    if (c) atomicAdd(&gh[i], c);
+  if (len <= kTopK) {
+    if (slice == 0) copy_short_row<kTs>(pt_row(a, row), a.out + static_cast<int64_t>(row) * kTopK, len);
+    return;
   }
-  if (threadIdx.x == 0) {
-    if (pos) atomicAdd(&a.gcnt[2 * row], pos);
-    if (zeros) atomicAdd(&a.gcnt[2 * row + 1], zeros);
+  int begin, end, n_sl;
+  if (!split_slice(len, a.S, slice, begin, end, n_sl)) return;
+
+  const RowSrc r = row_src(a, row, len);
+  const RowSrc rr = row_src(a, row, end);
+  const int b0 = begin + tid * 4;
+  SampleLoads<kTs> smp;
+  sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
+  Batch x0, x1;
+  load_batch<kVec, kTs>(rr, b0, x0);
+  load_batch<kVec, kTs>(rr, b0 + kStep, x1);
+  if (tid == 0) L.n[0] = 0;
+  const SampleLds S{L.u.res.hist, L.u.res.ck, L.wtot, L.res, L.misc};
+  const SampleCut cut = sample_threshold<kTs>(r, smp, S);
+  collect_ge<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, cut.thr, L.u.col.ck, L.u.col.ci, &L.n[0], kCapS, x0,
+                        x1);
+  __syncthreads();
+
+  const int n_loc = L.n[0];
+  int32_t* ctr = a.ctr + static_cast<int64_t>(row) * a.ctr_stride;
+  if (tid == 0) L.n[1] = n_loc ? atomicAdd(&ctr[1], n_loc) : 0;
+  __syncthreads();
+  uint32_t* lk = a.c_keys + static_cast<int64_t>(row) * kCapS;
+  int32_t* lt = a.c_tok + static_cast<int64_t>(row) * kCapS;
+  const int base = L.n[1];
+  const int n_put = min(n_loc, kCapS);
+  for (int i = tid; i < n_put; i += kTs) {
+    const int j = base + i;
+    if (j < kCapS) {
+      __hip_atomic_store(&lk[j], L.u.col.ck[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&lt[j], L.u.col.ci[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // Every wave's stores complete before the barrier, so the row's done count below comes after
+  // them; the CTA that completes the count reads them back with device-coherent loads.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const bool last = atomicAdd(&ctr[2], 1) == n_sl - 1;
+    L.n[2] = last;
+    L.n[3] = last ? __hip_atomic_load(&ctr[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+  }
+  __syncthreads();
+  if (!L.n[2]) return;
+
+  const int n_tot = L.n[3];
+  const PtRow pt = pt_row(a, row);
+  int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
+  if (n_tot >= kTopK && n_tot <= kCapS) {  // block-uniform
+    resolve_cands(L.u.res, n_tot, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
+      k = __hip_atomic_load(&lk[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      t = __hip_atomic_load(&lt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    });
+  } else {
+    // the estimate missed: the exact path over the row, its tokens above the threshold bin
+    // staged in the upper half of the token list and at most kCapS / 2 candidates below
+    exact_row<kVec, kTs>(L.u.res, L.u.res.ci + kCapS / 2, kCapS / 2, r, pt, dst);
   }
 }
 
-// Per slice (balanced over the rows by split_assign): pass-1 threshold (from the row's
-// histogram), unordered collection, then the A
-// tokens go straight to the output and the candidates to the row's published list, both at
-// positions from the row's global counters.  The CTA that finishes the row's last slice
-// resolves the threshold over the published candidates (or re-reads the row if they exceed
-// kCapS; fast path: takes the lowest-index zeros).
 template <bool kVec>
 __global__ __launch_bounds__(kTs) void topk_split_kernel(const TopkArgs a) {
   __shared__ SplitLds L;
@@ -960,16 +1365,24 @@ int split_count(int64_t rows, int64_t width, int max_splits, int n_cu) {
 }
 
 // CTAs the balanced split kernel spreads the rows' tokens over (its grid adds one per row):
-// rows * S, capped so that the grid stays within ~3 resident CTAs per CU.
-int split_target(int64_t rows, int S, int n_cu) {
-  const int64_t fit = 3 * static_cast<int64_t>(n_cu) - rows;
+// rows * S, capped so that the whole grid is resident at once (per_cu CTAs per CU).
+int split_target(int64_t rows, int S, int n_cu, int per_cu) {
+  const int64_t fit = per_cu * static_cast<int64_t>(n_cu) - rows;
   int64_t t = rows * S;
   t = t < fit ? t : fit;
   return static_cast<int>(t < rows ? rows : t);
 }
 
+// CTAs of a kTs-thread kernel resident per CU (the runtime's occupancy calculator).
+template <typename Kernel>
+int resident_per_cu(Kernel kernel) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kTs, 0) != hipSuccess || n < 1) n = 1;
+  return n;
+}
+
 struct WsLayout {
-  size_t ghist, gcnt, ctr, c_keys, c_tok, total;
+  size_t ctr, c_keys, c_tok, total;
 };
 
 WsLayout ws_layout(int64_t rows) {
@@ -980,8 +1393,6 @@ WsLayout ws_layout(int64_t rows) {
     off += (bytes + 255) / 256 * 256;
     return o;
   };
-  l.ghist = take(sizeof(int32_t) * rows * kBins);
-  l.gcnt = take(sizeof(int32_t) * rows * 2);
   l.ctr = take(sizeof(int32_t) * rows * 4);
   l.c_keys = take(sizeof(uint32_t) * rows * kCapS);
   l.c_tok = take(sizeof(int32_t) * rows * kCapS);
@@ -1029,7 +1440,7 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
 
   if (pre_hist != nullptr) {
     // [ghist1 rows*4096 | ghist2 rows*4096 | cnt rows*2]; words 0..2 of each ghist2 row are the
-    // row's split counters (zeroed by the logits call that built pass 1).
+    // row's split counters (zeroed by the logits call); ghist1 / cnt hold pass 1 if pass1_done.
     a.ghist = pre_hist;
     a.ctr = pre_hist + rows * kBins;
     a.ctr_stride = kBins;
@@ -1051,22 +1462,29 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
   DSA_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "%s: workspace must be 16-B aligned", who);
   char* ws = static_cast<char*>(workspace);
   if (!pre_hist) {
-    a.ghist = reinterpret_cast<int32_t*>(ws + l.ghist);
-    a.gcnt = reinterpret_cast<int32_t*>(ws + l.gcnt);
     a.ctr = reinterpret_cast<int32_t*>(ws + l.ctr);
     a.ctr_stride = 4;
+    hipLaunchKernelGGL(topk_zero_kernel, dim3(static_cast<uint32_t>((4 * rows + 255) / 256)), dim3(256), 0, stream,
+                       a.ctr, static_cast<int>(rows));
   }
   a.c_keys = reinterpret_cast<uint32_t*>(ws + l.c_keys);
   a.c_tok = reinterpret_cast<int32_t*>(ws + l.c_tok);
-  a.T = split_target(rows, S, n_cu);
-  const dim3 grid_bal(static_cast<uint32_t>(a.T + rows));
-  if (!pre_hist) hipLaunchKernelGGL(topk_zero_kernel, grid_rows, dim3(256), 0, stream, a.ghist, a.gcnt, a.ctr, a.ctr_stride);
-  if (!pass1_done) {
-    if (vec) hipLaunchKernelGGL((topk_split_hist_kernel<true>), grid_bal, dim3(kTs), 0, stream, a);
-    else hipLaunchKernelGGL((topk_split_hist_kernel<false>), grid_bal, dim3(kTs), 0, stream, a);
+  if (pre_hist && pass1_done) {  // the exact threshold bin from the logits kernel's pass 1
+    static const int per_cu_v = resident_per_cu(topk_split_kernel<true>);
+    static const int per_cu_s = resident_per_cu(topk_split_kernel<false>);
+    a.T = split_target(rows, S, n_cu, vec ? per_cu_v : per_cu_s);
+    const dim3 grid(static_cast<uint32_t>(a.T + rows));
+    if (vec) hipLaunchKernelGGL((topk_split_kernel<true>), grid, dim3(kTs), 0, stream, a);
+    else hipLaunchKernelGGL((topk_split_kernel<false>), grid, dim3(kTs), 0, stream, a);
+  } else {
+    static const int per_cu_v = resident_per_cu(topk_split_sampled_kernel<true>);
+    static const int per_cu_s = resident_per_cu(topk_split_sampled_kernel<false>);
+    const int64_t fit = (vec ? per_cu_v : per_cu_s) * static_cast<int64_t>(n_cu) / rows;
+    a.S = static_cast<int>(S < fit ? S : (fit > 1 ? fit : 1));
+    const dim3 grid(static_cast<uint32_t>(rows * a.S));
+    if (vec) hipLaunchKernelGGL((topk_split_sampled_kernel<true>), grid, dim3(kTs), 0, stream, a);
+    else hipLaunchKernelGGL((topk_split_sampled_kernel<false>), grid, dim3(kTs), 0, stream, a);
   }
-  if (vec) hipLaunchKernelGGL((topk_split_kernel<true>), grid_bal, dim3(kTs), 0, stream, a);
-  else hipLaunchKernelGGL((topk_split_kernel<false>), grid_bal, dim3(kTs), 0, stream, a);
   return check_launch(who);
 }
 

@@ -108,3 +108,40 @@ def test_topk_pass1_pairing(gpu, monkeypatch, fused, group, lens):
     ref = _oracle(lg.cpu(), mask.cpu(), case.context_lens, case.page_table_1(), case.width)
     assert np.array_equal(sorted_rows(paired.cpu().numpy()), sorted_rows(ref))
     assert np.array_equal(sorted_rows(plain.cpu().numpy()), sorted_rows(ref))
+
+
+def _sample_tokens(L):
+    """Tokens the sampled threshold reads in a row of L > 4096 tokens: 256 chunks of 16 aligned
+    tokens at ((2c + 1) L / 512) & ~15, the last ones clamped to (L - 16) & ~15."""
+    starts = [min(((2 * c + 1) * L // 512) & ~15, (L - 16) & ~15) for c in range(256)]
+    return np.unique(np.concatenate([np.arange(s, s + 16) for s in starts]))
+
+
+@pytest.mark.parametrize("pattern", ["sample_high", "sample_low"])
+def test_topk_sampled_threshold_fallback(gpu, pattern):
+    """Scores placed against the sample: high exactly where it looks (K* lands above all but a
+    few hundred keys: too few collected) or low there (K* lands below almost every key: too many
+    collected).  Both take the exact path; the sets still match the oracle for every split."""
+    B, W = 6, 65536 + 64
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(B, W, generator=g)
+    lengths = torch.tensor([65536, 40000, 16384, 9000, 4097, 70000 - 9000], dtype=torch.int32)
+    for b in range(B):
+        L = int(lengths[b])
+        s = torch.from_numpy(_sample_tokens(L))
+        if pattern == "sample_high":
+            x[b, s] += 10.0
+        else:
+            keep = torch.ones(W, dtype=torch.bool)
+            keep[s] = False
+            x[b, keep] += 10.0
+    mask = torch.full((B, (W + 15) // 16), -1, dtype=torch.int16)
+    pt = (torch.arange(W, dtype=torch.int32)[None, :] + 7 + 1000000 * torch.arange(B, dtype=torch.int32)[:, None])
+    ref = sorted_rows(_oracle(x, mask, lengths, pt, W))
+    xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
+    for name, fn in IMPLS.items():
+        got = sorted_rows(fn(xg, mg, lg, pg, cu).cpu().numpy())
+        assert np.array_equal(got, ref), f"{pattern} impl={name}"
+    got = hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1)
+    assert np.array_equal(sorted_rows(got.cpu().numpy()), ref), f"{pattern} dense"
