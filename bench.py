@@ -101,7 +101,7 @@ class DecodeStep:
 
     def logits_only(self, hist=False):
         """The dominant kernel alone (the step's launch shape, q already quantised); hist=True also
-        prepares the paired top-k's pass-1 workspace, as inside the step."""
+        prepares the paired top-k's workspace (its counters zeroed), as inside the step."""
         if not hasattr(self, "_q8"):
             self._q8, self._w8 = self.h.quant_q_fp8(self.q, self.w)
         c = self.case
@@ -357,7 +357,7 @@ def main(argv=None):
     log(f"timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
 
     if decode:
-        # the launch as the step makes it: logits + the paired top-k's pass-1 workspace
+        # the launch as the step makes it: logits + the paired top-k's counters zeroed
         k_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
         k0_ms = kernel_time_ms(step.logits_only, torch)
         kb = step.logits_bytes()
@@ -366,7 +366,7 @@ def main(argv=None):
         roofline = {"bound": "hbm", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": traffic, "traffic_source": tsrc, "algorithmic_bytes": kb,
-                    "kernel_us": round(k_ms * 1e3, 2), "without_pass1_workspace_us": round(k0_ms * 1e3, 2)}
+                    "kernel_us": round(k_ms * 1e3, 2), "without_topk_workspace_us": round(k0_ms * 1e3, 2)}
         pb = step.path_bytes()
         pa = pb / (ms / 1e3) / 1e9
         path = {"bound": "hbm", "achieved": round(pa, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

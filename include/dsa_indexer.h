@@ -103,8 +103,8 @@ int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* s
  * hist_ws (nullable, int32 [B * (2 * 4096 + 2)], 16-B aligned): the pass-1 workspace of a
  * following dsa_topk_transform_pre, in its layout [12-bit histograms rows*4096 | second block
  * rows*4096 | (positives, zeros) rows*2]; of the second block only words 0..2 of each row are
- * used (the split top-k's per-row counters).  fuse_pass1 = 0: hist_ws is zeroed (the top-k
- * builds pass 1); fuse_pass1 = 1 (needs hist_lens, int32 [B], and rows_per_cta <= 3): pass 1
+ * used (the split top-k's per-row counters).  fuse_pass1 = 0: only those counters are zeroed
+ * (the top-k then selects with its sampled threshold, no pass 1); fuse_pass1 = 1 (needs hist_lens, int32 [B], and rows_per_cta <= 3): pass 1
  * (12-bit key histogram + positive / zero counts of every row whose min(hist_lens[r], width) >
  * 2048) is built here, inside the logits kernel (reference: the fused kHist path). */
 int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t batch,
@@ -160,7 +160,8 @@ int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
  * dsa_mqa_logits_decode(hist_lens = lengths) (replaces
  * _C.sparse_mask_topk_transform_split_pre, sparse_mask_topk.cu:986-1051).  hist_ws is the
  * int32 [rows * (2 * 4096 + 2)] buffer given to the logits call; pass1_done says whether that
- * call built pass 1 (fuse_pass1), else pass 1 is built here into it (the logits call zeroed it).
+ * call built pass 1 (fuse_pass1: selection against its exact threshold bin), else the row is
+ * selected with the sampled threshold (the logits call zeroed the counters).
  * Its per-row counters are consumed, so a hist_ws serves one top-k call; `workspace` as above. */
 int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t width,
                            const int16_t* mask, int64_t mask_stride, const int32_t* lengths,

@@ -42,8 +42,8 @@ void check_kv(const torch::Tensor& kv_cache) {
 // ------------------------------------------------------------------------------------------------
 // Logits (hcu_ops/csrc/mqa_hist.cu:324-405).  persistent_ctas > 0 sets the number of CTAs the
 // K pages are spread over (<= 0: every CTA resident at once).  hist_lens: also return zws, the
-// top-k's pass-1 workspace, zeroed (the paired top-k builds pass 1) or, with fuse_pass1, with
-// pass 1 built inside the logits kernel.
+// top-k's workspace, its per-row counters zeroed (the paired top-k selects with its sampled
+// threshold) or, with fuse_pass1, with pass 1 built inside the logits kernel.
 std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::Tensor& kv_cache,
                                            const torch::Tensor& weights, const torch::Tensor& context_lens,
                                            const torch::Tensor& block_table, int64_t max_context_len,
@@ -295,7 +295,7 @@ torch::Tensor mqa_logits_prefill(const torch::Tensor& q, const torch::Tensor& we
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mqa_logits_hist", &mqa_logits_hist,
         "paged fp8 MQA indexer logits + 16-token nonzero mask -> {logits, mask, zws}; with hist_lens zws is the "
-        "paired top-k's pass-1 workspace (zeroed, or filled when fuse_pass1)",
+        "paired top-k's workspace (counters zeroed, or pass 1 filled when fuse_pass1)",
         py::arg("q"), py::arg("kv_cache"), py::arg("weights"), py::arg("context_lens"), py::arg("block_table"),
         py::arg("max_context_len"), py::arg("group_size"), py::arg("persistent_ctas"), py::arg("rows_per_cta"),
         py::arg("hist_lens"), py::arg("fuse_pass1") = false);

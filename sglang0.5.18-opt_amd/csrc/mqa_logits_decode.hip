@@ -112,7 +112,7 @@ struct DecodeArgs {
   int target;    // T: CTAs the pages are spread over
   const int32_t* hist_lens;
   int32_t* hist_ws;   // kHist: the fused pass-1 workspace
-  int32_t* zero_ws;   // non-null: a pass-1 workspace the top-k fills, zeroed here
+  int32_t* zero_ws;   // non-null: the paired top-k's workspace, whose counters are zeroed here
   int64_t batch;
 };
 
@@ -245,21 +245,13 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     }
   }
 
-  // The top-k's pass-1 workspace [histograms rows*4096 | counters rows*4096 | counts rows*2],
-  // a share per CTA: the histograms in 16-B stores, counter words 0..2 and the counts per row.
-  // Issued after the CTA's page stream: in the prologue the first DMA wait (vmcnt counts
-  // stores too) would wait for these stores as well.
+  // The paired top-k's per-row counters (words 0..2 of each row of the workspace's second
+  // block [histograms rows*4096 | counters rows*4096 | counts rows*2]), a row per CTA; issued
+  // after the CTA's page stream, so that no DMA wait covers these stores.
   auto zero_share = [&]() {
     if (a.zero_ws == nullptr) return;
-    const int64_t units = a.batch * (kBins / 4);
-    const int64_t u0 = units * cta / gridDim.x;
-    const int64_t u1 = units * (cta + 1) / gridDim.x;
-    int4* h4 = reinterpret_cast<int4*>(a.zero_ws);
-    for (int64_t u = u0 + tid; u < u1; u += NT) h4[u] = make_int4(0, 0, 0, 0);
-    for (int64_t rr = cta; rr < a.batch; rr += gridDim.x) {
+    for (int64_t rr = cta; rr < a.batch; rr += gridDim.x)
       if (tid < 3) a.zero_ws[(a.batch + rr) * kBins + tid] = 0;
-      if (tid < 2) a.zero_ws[2 * a.batch * kBins + 2 * rr + tid] = 0;
-    }
   };
   __syncthreads();
   const int grp = s_assign[0];

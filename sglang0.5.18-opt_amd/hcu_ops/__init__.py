@@ -26,9 +26,9 @@ _TOPK_SPLITS = int(os.environ.get("HCU_TOPK_SPLITS", "8"))
 # slice of one request); <= 0 uses twice the CU count.  HCU_MQA_RPC: rows sharing one K stream
 # for groups (must divide the group).
 # HCU_MQA_HIST_MAX_ROWS: up to this many rows, mqa_logits(..., hist_lens) hands the paired top-k a
-# pass-1 workspace that it zeroed (saving the top-k's zeroing launch); HCU_MQA_FUSED_PASS1=1
-# builds pass 1 inside the logits kernel instead (slower on gfx950: its LDS histogram lowers the
-# logits kernel's occupancy).
+# workspace whose counters it zeroed (saving the top-k's zeroing launch; the top-k then selects
+# with its sampled threshold); HCU_MQA_FUSED_PASS1=1 builds the exact pass 1 inside the logits
+# kernel instead (slower on gfx950: its LDS histogram lowers the logits kernel's occupancy).
 _MQA_PCTAS = int(os.environ.get("HCU_MQA_PCTAS", "0"))
 _MQA_PCTAS_G1 = int(os.environ.get("HCU_MQA_PCTAS_G1", str(_MQA_PCTAS)))
 _MQA_RPC = int(os.environ.get("HCU_MQA_RPC", "2"))
@@ -84,7 +84,7 @@ def mqa_logits(q, kv_cache, weights, context_lens, block_table, max_context_len,
     (reference hcu_ops/hcu_ops/__init__.py:82-105).
 
     hist_lens: lengths of the paired sparse_mask_topk_transform; when that call will split rows,
-    its pass-1 workspace is prepared here (zeroed, or filled when HCU_MQA_FUSED_PASS1=1)."""
+    its workspace is prepared here (counters zeroed, or pass 1 filled when HCU_MQA_FUSED_PASS1=1)."""
     global _MQA_HIST
     rows = q.shape[0]
     if persistent_ctas is None:

@@ -101,16 +101,32 @@ def test_decode_fused_histogram(gpu, monkeypatch, group, lens):
 
 
 @pytest.mark.parametrize("group,lens", [(1, [9000, 100, 40000]), (2, [20000, 3000, 0, 0])])
-def test_decode_pass1_workspace_zeroed(gpu, monkeypatch, group, lens):
-    """Without the fused pass 1 the logits call hands over the pass-1 workspace zeroed."""
-    monkeypatch.setattr(hcu_ops, "_MQA_FUSED_PASS1", False)
+def test_decode_topk_counters_zeroed(gpu, group, lens):
+    """Without the fused pass 1 the logits call (C ABI, hist_ws given, fuse_pass1 = 0) zeroes
+    exactly the paired top-k's per-row counters (words 0..2 of each row of the second block)
+    and writes nothing else of the workspace."""
+    import ctypes
+    import os
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(hcu_ops.__file__), "libdsa_indexer.so"))
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    f = lib.dsa_mqa_logits_decode
+    f.argtypes = [P, P, I, I64, I, P, I64, P, P, I64, I64, P, I64, P, I64, I, I, P, P, I, P]
+    lib.dsa_last_error.restype = ctypes.c_char_p
     case = wl.decode_case(14, lens, group=group, heads=64)
-    _, _, lg, mask = _run_decode(case, gpu, hist=True)
-    assert hcu_ops._MQA_HIST is not None and hcu_ops._MQA_HIST[3] is False
-    B = case.rows
-    zws = hcu_ops._MQA_HIST[2].cpu().numpy()
-    assert not zws[:B * 4096].any() and not zws[2 * B * 4096:].any()
-    assert not zws[B * 4096:2 * B * 4096].reshape(B, 4096)[:, :3].any()
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    kv, ctx, bt = case.kv.to(gpu), case.context_lens.to(gpu), case.block_table.to(gpu)
+    B, W = case.rows, case.width
+    lg = torch.empty(B, W, device=gpu)
+    mask = torch.empty(B, W // 16, dtype=torch.int16, device=gpu)
+    ws = torch.full((B * (2 * 4096 + 2),), -1, dtype=torch.int32, device=gpu)
+    st = f(q8.data_ptr(), w.data_ptr(), 64, B, group, kv.data_ptr(), kv.stride(0), ctx.data_ptr(), bt.data_ptr(),
+           bt.stride(0), bt.shape[1], lg.data_ptr(), lg.stride(0), mask.data_ptr(), mask.stride(0),
+           1 if group == 1 else 2, 0, ctx.data_ptr(), ws.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.dsa_last_error()
+    zws = ws.cpu().numpy()
+    ctr = zws[B * 4096:2 * B * 4096].reshape(B, 4096)
+    assert not ctr[:, :3].any(), "top-k counters not zeroed"
+    assert (ctr[:, 3:] == -1).all() and (zws[:B * 4096] == -1).all() and (zws[2 * B * 4096:] == -1).all()
     _check_decode(case, lg, mask)
 
 
