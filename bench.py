@@ -278,7 +278,8 @@ def kernel_time_ms(fn, torch, reps=20, rounds=5):
     with torch.cuda.graph(g):
         for _ in range(reps):
             fn()
-    g.replay()
+    for _ in range(3):  # first replays of a new graph run slow (fresh buffers, clocks)
+        g.replay()
     torch.cuda.synchronize()
     times = []
     for _ in range(rounds):

@@ -542,16 +542,36 @@ __device__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x,
 
 // Keys >= thr of a batch into the LDS list (ck, ci) at slots from one wave-aggregated atomic;
 // the count keeps growing past cap (the caller sees the overflow), the stores stop at cap.
-template <int NT>
+// key(x) >= thr is decided on the raw float bits, the key transform folded into the threshold:
+// keys of floats with the sign clear order like their bits as signed integers, keys of negative
+// floats the other way round.  kPos (thr >= key of +0): pass iff (int)bits >= (int)(thr ^ 2^31);
+// otherwise every float with the sign clear passes and a negative one iff bits <= ~thr.  A
+// masked-out token (key +0) passes iff +0 >= thr, i.e. iff !kPos or thr == key of +0.
+template <int NT, bool kPos>
 __device__ __forceinline__ void process_ge(const RowSrc& rr, int b, const Batch& x, uint32_t thr, uint32_t* ck,
                                            int* ci, int* n, int cap) {
-  uint32_t k[kUnroll][4];
+  const int lo = static_cast<int>(thr ^ kZeroKey);
+  const uint32_t hi = ~thr;
+  const bool zero_in = kZeroKey >= thr;
   uint32_t f = 0;
+  uint32_t mq[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const uint32_t v = quad_keys(rr, b + u * NT * 4, x.q[u], k[u]);
+    const int i0 = b + u * NT * 4;
+    const int safe = i0 < rr.len ? i0 : 0;
+    mq[u] = ((x.q[u].mw | rr.mask_or) >> (safe & 15)) & 0xFu;  // mask bits of the quad
+    const int rem = rr.len - i0;
+    const uint32_t valid = rem <= 0 ? 0u : (rem < 4 ? (1u << rem) - 1u : 0xFu);
+    uint32_t pass = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f |= static_cast<uint32_t>(((v >> j) & 1u) && k[u][j] >= thr) << (u * 4 + j);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t bits = __float_as_uint(x.q[u].v[j]);
+      bool ge;
+      if constexpr (kPos) ge = static_cast<int>(bits) >= lo;
+      else ge = static_cast<int>(bits) >= 0 || bits <= hi;
+      pass |= static_cast<uint32_t>(((mq[u] >> j) & 1u) ? ge : zero_in) << j;
+    }
+    f |= (pass & valid) << (u * 4);
   }
   int t;
   int p = wave_prefix_5(__popc(f), t);
@@ -565,7 +585,7 @@ __device__ __forceinline__ void process_ge(const RowSrc& rr, int b, const Batch&
     for (int j = 0; j < 4; ++j) {
       if ((f >> (u * 4 + j)) & 1u) {
         if (p < cap) {
-          ck[p] = k[u][j];
+          ck[p] = ((mq[u] >> j) & 1u) ? float_key(x.q[u].v[j]) : kZeroKey;
           ci[p] = b + u * NT * 4 + j;
         }
         ++p;
@@ -577,8 +597,15 @@ __device__ __forceinline__ void process_ge(const RowSrc& rr, int b, const Batch&
 template <bool kVec, int NT>
 __device__ void collect_ge(const RowSrc& rr, int b, int n_batches, uint32_t thr, uint32_t* ck, int* ci, int* n,
                            int cap, Batch& x0, Batch& x1) {
-  stream_batches<kVec, NT>(rr, b, n_batches, x0, x1,
-                           [&](int bb, const Batch& x) { process_ge<NT>(rr, bb, x, thr, ck, ci, n, cap); });
+  if (thr >= kZeroKey) {  // block-uniform
+    stream_batches<kVec, NT>(rr, b, n_batches, x0, x1, [&](int bb, const Batch& x) {
+      process_ge<NT, true>(rr, bb, x, thr, ck, ci, n, cap);
+    });
+  } else {
+    stream_batches<kVec, NT>(rr, b, n_batches, x0, x1, [&](int bb, const Batch& x) {
+      process_ge<NT, false>(rr, bb, x, thr, ck, ci, n, cap);
+    });
+  }
 }
 
 // Radix select over LDS members: the key `thr` such that `need` members have key >= thr and the
