@@ -285,11 +285,8 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   const int n_local = p_end - p_begin;  // <= Sh::kMaxPages by the host's choice of target
   const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride + p_begin;
 
-  // the first page(s) of every stream in flight first, straight from the block table
+  // the first page of every stream in flight first, straight from the block table
   if (s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[s]) * a.page_stride, s_slot0[s], r, lane);
-  if constexpr (NS > 2) {
-    if (S + s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[S + s]) * a.page_stride, s_slot1[s], r, lane);
-  }
 
   // q / w fragments of this wave's row: lane l holds head ht*16 + l%16, bytes (l/16)*32 .. +32,
   // and the weights of heads ht*16 + 4*(l/16) + e, the rows of the MFMA result it holds.
@@ -307,14 +304,22 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     }
   }
 
-  for (int i = tid; i < n_local; i += NT) s_bt[i] = btr[i];
+  // The CTA's block-table slice straight into LDS (no register round trip, so nothing here
+  // waits for the loads above), then the second page of every stream: while the first pages
+  // are in flight, the memory system already has the next ones.  Step 0 waits for everything
+  // but that second page, and its barrier publishes s_bt and the zeroed counters; no barrier
+  // is needed here.
+  for (int b = wave * kWave; b < n_local; b += NT)
+    if (b + lane < n_local) __builtin_amdgcn_global_load_lds(btr + b + lane, &s_bt[b], 4, 0, 0);
+  if (S + s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[S + s]) * a.page_stride, s_slot1[s], r, lane);
   if constexpr (kHist) {
     for (int i = tid; i < R * kBins / 2; i += NT) s_hist[i] = 0;
     if (tid < 2 * R) s_cnt[tid] = 0;
   }
   // Mask words of the group's rows past its pages (no CTA scores them) are zeroed by the
   // group's CTAs, a share each: one 8-B store per page and row when the layout allows it.
-  {
+  // Issued after the page stream, so that no DMA wait covers these stores.
+  auto zero_mask_tail = [&]() {
     const int tail = a.bt_pages - pages;
     const int units = R * tail;
     const int u0 = static_cast<int>(static_cast<int64_t>(units) * jc / nj);
@@ -330,8 +335,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
         for (int e = 0; e < 4; ++e) m[e] = 0;
       }
     }
-  }
-  __syncthreads();
+  };
 
   int nz = 0, pos = 0;
   const int n_steps = (n_local + S - 1) / S;  // block-uniform
@@ -367,9 +371,10 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   auto step = [&](int k, uint8_t* cur, uint8_t* nxt) {
     const int i = k * S + s;  // this stream's page (local index)
     // this wave's share of page i has landed: the only VMEM ops issued after it are the DMAs of
-    // the pages still ahead of it (NS = 3: page i + S, if it exists).  The barrier publishes
-    // every wave's share and retires the readers of `nxt` from the previous step.
-    if (NS > 2 && i + S < n_local) wait_vmcnt(n_dma);
+    // the pages still ahead of it (page i + S at step 0, or always with NS = 3, if it exists).
+    // The barrier publishes every wave's share and retires the readers of `nxt` from the
+    // previous step.
+    if ((NS > 2 || k == 0) && i + S < n_local) wait_vmcnt(n_dma);
     else wait_vmcnt(0);
     // a bare s_barrier: __syncthreads' release fence would wait for every LDS DMA in flight
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS histogram updates are done
@@ -377,7 +382,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     flush();
-    if (i + (NS - 1) * S < n_local)
+    if (i + (NS - 1) * S < n_local && (NS > 2 || k > 0))  // NS = 2: page S + s came with the prologue
       dma_page<R>(a.kv + static_cast<int64_t>(s_bt[i + (NS - 1) * S]) * a.page_stride, nxt, r, lane);
     if (i >= n_local) return;  // stream-uniform (the stream still takes part in the barriers)
     const float scale = reinterpret_cast<const float*>(cur + kPageFp8Bytes)[lane];
@@ -418,6 +423,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     }
   }
   flush();
+  zero_mask_tail();
   zero_share();
 
   if constexpr (kHist) {
