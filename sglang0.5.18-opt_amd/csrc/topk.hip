@@ -1025,10 +1025,9 @@ __device__ __attribute__((noinline)) void exact_row(ResolveLds<NT, CAP>& L, int*
 }
 
 // ---------------------------------------------------------------------------------------------
-// One CTA per row.  kPre: pass 1 (histogram + counts) comes from a.ghist / a.gcnt and the row
-// is collected against its exact threshold bin; otherwise against the sampled threshold K*
-// (one read of the row), with the exact path when the collected count misses [2048, kCapC].
-template <bool kVec, bool kPre>
+// One CTA per row with pass 1 (histogram + counts) from a.ghist / a.gcnt (the logits kernel's
+// fused pass 1): the row is collected against its exact threshold bin.
+template <bool kVec>
 __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   __shared__ ResolveLds<kTk, kCapC> L;
   __shared__ int s_a[kTopK];
@@ -1045,62 +1044,81 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   const int b0 = static_cast<int>(threadIdx.x) * 4;
   const int n_batches = (len + kStep - 1) / kStep;
   Batch x0, x1;
-  if constexpr (kPre) {
-    // pass-1 slots (4 bins per thread) first, then the first two batches, so that waiting for
-    // the histogram does not wait for the batches
-    const int4 h4 = reinterpret_cast<const int4*>(a.ghist + static_cast<int64_t>(row) * kBins)[threadIdx.x];
-    const int pos = a.gcnt[2 * row];
-    const int zeros = a.gcnt[2 * row + 1];
-    load_batch<kVec, kTk>(r, b0, x0);
-    load_batch<kVec, kTk>(r, b0 + kStep, x1);
-    Meta m;
-    m.pos = pos;
-    m.fast = pos <= kTopK && pos + zeros >= kTopK;
-    m.t1 = 0;
-    m.above1 = pos;
-    if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
-    if (!m.fast) {
-      const int h[4] = {h4.x, h4.y, h4.z, h4.w};
-      find_threshold_regs<kTk, 4>(h, kTopK, L.wtot, L.res);
-      m.t1 = static_cast<uint32_t>(L.res[0]);
-      m.above1 = L.res[1];
-    } else {
-      __syncthreads();
-    }
-    Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
-    collect<kVec, kTk>(r, b0, n_batches, m, st, x0, x1);
-    __syncthreads();
-    const int n_a = min(L.misc[0], kTopK);
-    const int n_c = L.misc[1];
-    for (int i = threadIdx.x; i < n_a; i += kTk) put(dst, i, pt[s_a[i]]);
-    if (m.fast) {
-      ordered_scan<kVec, kTk>(
-          r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
-    } else if (n_c <= kCapC) {
-      resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
-    } else {
-      resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
-    }
+  // pass-1 slots (4 bins per thread) first, then the first two batches, so that waiting for
+  // the histogram does not wait for the batches
+  const int4 h4 = reinterpret_cast<const int4*>(a.ghist + static_cast<int64_t>(row) * kBins)[threadIdx.x];
+  const int pos = a.gcnt[2 * row];
+  const int zeros = a.gcnt[2 * row + 1];
+  load_batch<kVec, kTk>(r, b0, x0);
+  load_batch<kVec, kTk>(r, b0 + kStep, x1);
+  Meta m;
+  m.pos = pos;
+  m.fast = pos <= kTopK && pos + zeros >= kTopK;
+  m.t1 = 0;
+  m.above1 = pos;
+  if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
+  if (!m.fast) {
+    const int h[4] = {h4.x, h4.y, h4.z, h4.w};
+    find_threshold_regs<kTk, 4>(h, kTopK, L.wtot, L.res);
+    m.t1 = static_cast<uint32_t>(L.res[0]);
+    m.above1 = L.res[1];
   } else {
-    SampleLoads<kTk> smp;
-    sample_issue<kVec, kTk>(r, smp);  // the sample first: it is needed first
-    load_batch<kVec, kTk>(r, b0, x0);
-    load_batch<kVec, kTk>(r, b0 + kStep, x1);
-    const SampleLds S{L.hist, L.ck, L.wtot, L.res, L.misc};
-    const SampleCut cut = sample_threshold<kTk>(r, smp, S);
-    if (threadIdx.x == 0) L.misc[2] = 0;
     __syncthreads();
-    collect_ge<kVec, kTk>(r, b0, n_batches, cut.thr, L.ck, L.ci, &L.misc[2], kCapC, x0, x1);
-    __syncthreads();
-    const int n = L.misc[2];
-    if (n >= kTopK && n <= kCapC) {  // block-uniform
-      resolve_cands(L, n, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
-        k = L.ck[e];
-        t = L.ci[e];
-      });
-    } else {
-      exact_row<kVec, kTk>(L, s_a, kCapC, r, pt, dst);
-    }
+  }
+  Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
+  collect<kVec, kTk>(r, b0, n_batches, m, st, x0, x1);
+  __syncthreads();
+  const int n_a = min(L.misc[0], kTopK);
+  const int n_c = L.misc[1];
+  for (int i = threadIdx.x; i < n_a; i += kTk) put(dst, i, pt[s_a[i]]);
+  if (m.fast) {
+    ordered_scan<kVec, kTk>(
+        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
+  } else if (n_c <= kCapC) {
+    resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
+  } else {
+    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
+  }
+}
+
+// One 512-thread CTA per row against the sampled threshold K* (one read of the row), with the
+// exact path when the collected count misses [2048, kCapS].  Two CTAs share a CU, so one's
+// latency-bound phases (sample, resolution) overlap the other's collection.
+template <bool kVec>
+__global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void topk_row_sampled_kernel(
+    const TopkArgs a) {
+  __shared__ ResolveLds<kTs, kCapS> L;
+  __shared__ int s_a[kTopK];
+  constexpr int kStep = kTs * 4 * kUnroll;
+  const int row = blockIdx.x;
+  const int len = row_len(a, row);
+  const PtRow pt = pt_row(a, row);
+  int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
+  if (len <= kTopK) {
+    copy_short_row<kTs>(pt, dst, len);
+    return;
+  }
+  const RowSrc r = row_src(a, row, len);
+  const int b0 = static_cast<int>(threadIdx.x) * 4;
+  SampleLoads<kTs> smp;
+  sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
+  Batch x0, x1;
+  load_batch<kVec, kTs>(r, b0, x0);
+  load_batch<kVec, kTs>(r, b0 + kStep, x1);
+  const SampleLds S{L.hist, L.ck, L.wtot, L.res, L.misc};
+  const SampleCut cut = sample_threshold<kTs>(r, smp, S);
+  if (threadIdx.x == 0) L.misc[2] = 0;
+  __syncthreads();
+  collect_ge<kVec, kTs>(r, b0, (len + kStep - 1) / kStep, cut.thr, L.ck, L.ci, &L.misc[2], kCapS, x0, x1);
+  __syncthreads();
+  const int n = L.misc[2];
+  if (n >= kTopK && n <= kCapS) {  // block-uniform
+    resolve_cands(L, n, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
+      k = L.ck[e];
+      t = L.ci[e];
+    });
+  } else {
+    exact_row<kVec, kTs>(L, s_a, kCapS, r, pt, dst);
   }
 }
 
@@ -1475,11 +1493,11 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
   }
   if (S <= 1) {
     if (pre_hist && pass1_done) {
-      if (vec) hipLaunchKernelGGL((topk_single_kernel<true, true>), grid_rows, dim3(kTk), 0, stream, a);
-      else hipLaunchKernelGGL((topk_single_kernel<false, true>), grid_rows, dim3(kTk), 0, stream, a);
+      if (vec) hipLaunchKernelGGL((topk_single_kernel<true>), grid_rows, dim3(kTk), 0, stream, a);
+      else hipLaunchKernelGGL((topk_single_kernel<false>), grid_rows, dim3(kTk), 0, stream, a);
     } else {
-      if (vec) hipLaunchKernelGGL((topk_single_kernel<true, false>), grid_rows, dim3(kTk), 0, stream, a);
-      else hipLaunchKernelGGL((topk_single_kernel<false, false>), grid_rows, dim3(kTk), 0, stream, a);
+      if (vec) hipLaunchKernelGGL((topk_row_sampled_kernel<true>), grid_rows, dim3(kTs), 0, stream, a);
+      else hipLaunchKernelGGL((topk_row_sampled_kernel<false>), grid_rows, dim3(kTs), 0, stream, a);
     }
     return check_launch(who);
   }
