@@ -389,11 +389,12 @@ __device__ void collect(const RowSrc& rr, int b, int n_batches, const Meta& m, c
 // two-pass path instead, so the result never depends on the sample.
 //
 // Sample: 256 chunks of 16 aligned tokens spread evenly over the row (one 64-B sector of
-// scores and one mask word each), or the whole row when it has <= 4096 tokens.  K* is the
-// sample key of rank k (descending) with k = mu + 4 sqrt(mu) + 2, mu = 2048 * 4096 / len the
-// expected number of sample keys above the row's 2048th key: the row has fewer than 2048 keys
-// >= K* only if the sample holds >= k keys above the 2048th, a 4-sigma binomial event, and
-// about len * k / 4096 ~ 2048 + 4.5 sqrt(2048 len / 4096) keys are collected.
+// scores and one mask word each), or the whole row when it has <= 4096 tokens.  K* is the lower
+// edge of the 4096-key digit (key[31:12]) holding the sample key of rank k (descending), k =
+// mu + 4 sqrt(mu) + 2, mu = 2048 * 4096 / len the expected number of sample keys above the row's
+// 2048th key: the row has fewer than 2048 keys >= K* only if the sample holds >= k keys above
+// the 2048th, a 4-sigma binomial event, and about len * k / 4096 ~ 2048 + 4.5 sqrt(2048 len /
+// 4096) keys are collected (plus the few of that digit below the rank-k key).
 constexpr int kSampleChunks = 256;
 constexpr int kSample = kSampleChunks * 16;
 
@@ -435,13 +436,11 @@ __device__ __forceinline__ uint32_t cand_digit(uint32_t key, const SampleCut& c)
   return d < 4095u ? d : 4095u;
 }
 
-// Scratch of the threshold search (LDS): a 12-bit histogram and the keys of one bin's members.
+// Scratch of the threshold search (LDS).
 struct SampleLds {
   int* hist;      // kBins
-  uint32_t* mk;   // NT, 16-B aligned
   int* wtot;      // NT / kWave
   int* res;       // 6
-  int* misc;      // 2
 };
 
 // This thread's share of a row's sample, loaded (sample_issue) but not yet used, so that the
@@ -472,7 +471,6 @@ __device__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x,
   const Quad* q = x.q;
   const int* i0 = x.i0;
   zero_lds<NT>(S.hist, kBins);
-  if (tid == 0) S.misc[0] = 0;
   __syncthreads();
   uint32_t k[QPT][4], v[QPT];
 #pragma unroll
@@ -487,56 +485,24 @@ __device__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x,
   const int needs[2] = {rank, sample_mid_rank(r.len)};
   find_thresholds<kBins, NT, 2>(S.hist, needs, S.wtot, S.res);
   const uint32_t b = static_cast<uint32_t>(S.res[0]);
-  const int need = rank - S.res[1];  // rank of K* within bin b, 1 .. count(b)
-  const int cnt = S.res[2];
+  const int need = rank - S.res[1];  // rank of the sample's K* within bin b, 1 .. count(b)
   const uint32_t bm = static_cast<uint32_t>(S.res[3]);  // bin of the 2048th-key estimate (>= b)
   const uint32_t span = bm > b ? bm - b + 1u : 1u;         // <= 4096
   SampleCut cut;
   cut.shift = 9 + (32 - __builtin_clz(span));              // 10 .. 22
-  if (cnt > NT) {  // block-uniform; a heavy bin: its lower edge (a superset)
-    cut.thr = b << 20;
-    return cut;
-  }
-  static_assert(QPT * 4 <= 16, "member masks hold 16 keys");
-  uint32_t fm = 0;
+  // second digit, key[19:12], over the members of bin b: K* is the lower edge of the digit that
+  // holds the rank-`need` member (at most one 4096-key digit below it is collected in excess)
+  if (tid < 256) S.hist[tid] = 0;
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < QPT; ++j) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) fm |= static_cast<uint32_t>(((v[j] >> e) & 1u) && (k[j][e] >> 20) == b) << (j * 4 + e);
-  }
-  {
-    int tm;
-    int pm = wave_prefix_5(__popc(fm), tm);
-    int base = 0;
-    if (tm != 0 && lane_id() == 0) base = atomicAdd(&S.misc[0], tm);
-    pm += uniform(base);
-#pragma unroll
-    for (int j = 0; j < QPT; ++j) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if ((fm >> (j * 4 + e)) & 1u) S.mk[pm++] = k[j][e];
-      }
-    }
+    for (int e = 0; e < 4; ++e)
+      if (((v[j] >> e) & 1u) && (k[j][e] >> 20) == b) atomicAdd(&S.hist[(k[j][e] >> 12) & 0xFFu], 1);
   }
   __syncthreads();
-  if (tid < cnt) {
-    const uint32_t x = S.mk[tid];
-    int gt = 0, eq = 0;
-    int i = 0;
-#pragma unroll 4
-    for (; i + 4 <= cnt; i += 4) {  // 16-B LDS reads
-      const uint4 y = *reinterpret_cast<const uint4*>(S.mk + i);
-      gt += (y.x > x) + (y.y > x) + (y.z > x) + (y.w > x);
-      eq += (y.x == x) + (y.y == x) + (y.z == x) + (y.w == x);
-    }
-    for (; i < cnt; ++i) {
-      gt += S.mk[i] > x;
-      eq += S.mk[i] == x;
-    }
-    if (gt < need && need <= gt + eq) S.misc[1] = static_cast<int>(x);
-  }
-  __syncthreads();
-  cut.thr = static_cast<uint32_t>(S.misc[1]);
+  find_threshold<256, NT>(S.hist, need, S.wtot, S.res);
+  cut.thr = (b << 20) | (static_cast<uint32_t>(S.res[0]) << 12);
   return cut;
 }
 
@@ -1105,7 +1071,7 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
   Batch x0, x1;
   load_batch<kVec, kTs>(r, b0, x0);
   load_batch<kVec, kTs>(r, b0 + kStep, x1);
-  const SampleLds S{L.hist, L.ck, L.wtot, L.res, L.misc};
+  const SampleLds S{L.hist, L.wtot, L.res};
   const SampleCut cut = sample_threshold<kTs>(r, smp, S);
   if (threadIdx.x == 0) L.misc[2] = 0;
   __syncthreads();
@@ -1244,7 +1210,7 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
   load_batch<kVec, kTs>(rr, b0, x0);
   load_batch<kVec, kTs>(rr, b0 + kStep, x1);
   if (tid == 0) L.n[0] = 0;
-  const SampleLds S{L.u.res.hist, L.u.res.ck, L.wtot, L.res, L.misc};
+  const SampleLds S{L.u.res.hist, L.wtot, L.res};
   const SampleCut cut = sample_threshold<kTs>(r, smp, S);
   collect_ge<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, cut.thr, L.u.col.ck, L.u.col.ci, &L.n[0], kCapS, x0,
                         x1);
