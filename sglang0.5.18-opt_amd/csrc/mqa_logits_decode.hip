@@ -131,17 +131,13 @@ __device__ __forceinline__ int group_ctas(int pages, int total_pages, int target
   return static_cast<int>((static_cast<int64_t>(pages) * target + total_pages - 1) / total_pages);
 }
 
-// Block-wide (NT threads) sum and exclusive prefix.
+// Block-wide (NT threads) sum and exclusive prefix; s_w (NT / 64 words) must not be reused
+// before the next barrier.
 template <int NT>
 __device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  int inc = x;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(inc, o);
-    if (lane >= o) inc += y;
-  }
+  const int inc = wave_prefix_sum(x);
   if (lane == 63) s_w[w] = inc;
   __syncthreads();
   int before = 0, tot = 0;
@@ -150,7 +146,6 @@ __device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
     before += v < w ? s_w[v] : 0;
     tot += s_w[v];
   }
-  __syncthreads();
   total = tot;
   return before + inc - x;
 }
@@ -210,7 +205,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   __shared__ __attribute__((aligned(16))) uint8_t s_slot2[NS > 2 ? S : 1][NS > 2 ? kPageBytes : 16];
   __shared__ uint32_t s_hist[kHist ? R * kBins / 2 : 1];  // 16-bit counters, two bins per word
   __shared__ int s_cnt[2 * R];
-  __shared__ int s_w[NT / kWave];
+  __shared__ int s_w[2][NT / kWave];
   __shared__ int s_assign[3];  // group, index within the group's CTAs, the group's CTA count
   __shared__ int s_bt[Sh::kMaxPages];
 
@@ -220,23 +215,49 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   const int cta = blockIdx.x;
 
   // ---- work assignment (identical in every CTA) ----
+  // Thread tid owns groups [g_lo, g_hi); their page counts are read once and kept (up to kGpt
+  // a thread, else re-read).
+  constexpr int kGpt = 4;
   const int per_t = (a.n_groups + NT - 1) / NT;
   const int g_lo = min(tid * per_t, a.n_groups);
   const int g_hi = min(g_lo + per_t, a.n_groups);
+  const bool cached = per_t <= kGpt;  // block-uniform
+  int gp[kGpt];
   int my_pages = 0;
-  for (int g = g_lo; g < g_hi; ++g) my_pages += group_pages(a, g);
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kGpt; ++i) {
+      gp[i] = g_lo + i < g_hi ? group_pages(a, g_lo + i) : 0;
+      my_pages += gp[i];
+    }
+  } else {
+    for (int g = g_lo; g < g_hi; ++g) my_pages += group_pages(a, g);
+  }
   int total_pages;
-  block_excl<NT>(my_pages, total_pages, s_w);
+  block_excl<NT>(my_pages, total_pages, s_w[0]);
   if (tid == 0) s_assign[0] = -1;
   int my_ctas = 0;
-  for (int g = g_lo; g < g_hi; ++g) my_ctas += group_ctas(group_pages(a, g), total_pages, a.target);
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kGpt; ++i) my_ctas += g_lo + i < g_hi ? group_ctas(gp[i], total_pages, a.target) : 0;
+  } else {
+    for (int g = g_lo; g < g_hi; ++g) my_ctas += group_ctas(group_pages(a, g), total_pages, a.target);
+  }
   int total_ctas;
-  int c0 = block_excl<NT>(my_ctas, total_ctas, s_w);
+  int c0 = block_excl<NT>(my_ctas, total_ctas, s_w[1]);
   if (cta >= c0 && cta < c0 + my_ctas) {
-    for (int g = g_lo; g < g_hi; ++g) {
-      const int n = group_ctas(group_pages(a, g), total_pages, a.target);
+    for (int i = 0; g_lo + i < g_hi; ++i) {
+      int p;
+      if (cached) {
+        p = gp[0];
+#pragma unroll
+        for (int j = 1; j < kGpt; ++j) p = i == j ? gp[j] : p;
+      } else {
+        p = group_pages(a, g_lo + i);
+      }
+      const int n = group_ctas(p, total_pages, a.target);
       if (cta < c0 + n) {
-        s_assign[0] = g;
+        s_assign[0] = g_lo + i;
         s_assign[1] = cta - c0;
         s_assign[2] = n;
         break;
