@@ -825,6 +825,37 @@ __device__ void resolve_cands(ResolveLds<NT, CAP>& L, int n, const SampleCut& cu
   }
 }
 
+// A row of at most kSample tokens: every key goes to the candidate list at its token's
+// position (no threshold, no collection pass) and is resolved on the plain 12-bit digit.
+template <bool kVec, int NT, int CAP>
+__device__ void small_row(ResolveLds<NT, CAP>& L, const RowSrc& r, const PtRow& pt, int32_t* dst) {
+  static_assert(CAP >= kSample, "the row fits the candidate list");
+  constexpr int QPT = kSample / 4 / NT;
+#pragma unroll
+  for (int j = 0; j < QPT; ++j) {
+    const int i0 = (static_cast<int>(threadIdx.x) + j * NT) * 4;
+    Quad q;
+    load_quad<kVec>(r, i0, q);
+    uint32_t k[4];
+    const uint32_t v = quad_keys(r, i0, q, k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if ((v >> e) & 1u) {
+        L.ck[i0 + e] = k[e];
+        L.ci[i0 + e] = i0 + e;
+      }
+    }
+  }
+  __syncthreads();
+  SampleCut cut;
+  cut.thr = 0u;
+  cut.shift = 20;
+  resolve_cands(L, r.len, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
+    k = L.ck[e];
+    t = L.ci[e];
+  });
+}
+
 // Ordered scan of the row for the first `remaining` tokens with key == thr that pass `cond`
 // (fast path: the zeros; rescan: the ties), written to dst[base + rank]; stops once enough
 // were found unless gt is set.  gt: also write the keys > thr that pass cond to
@@ -1065,6 +1096,10 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
     return;
   }
   const RowSrc r = row_src(a, row, len);
+  if (len <= kSample) {  // block-uniform
+    small_row<kVec, kTs>(L, r, pt, dst);
+    return;
+  }
   const int b0 = static_cast<int>(threadIdx.x) * 4;
   SampleLoads<kTs> smp;
   sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
@@ -1196,6 +1231,11 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
   const int len = row_len(a, row);
   if (len <= kTopK) {
     if (slice == 0) copy_short_row<kTs>(pt_row(a, row), a.out + static_cast<int64_t>(row) * kTopK, len);
+    return;
+  }
+  if (len <= kSample) {  // the whole row in one CTA, no split
+    if (slice == 0) small_row<kVec, kTs>(L.u.res, row_src(a, row, len), pt_row(a, row),
+                                         a.out + static_cast<int64_t>(row) * kTopK);
     return;
   }
   int begin, end, n_sl;
@@ -1366,7 +1406,9 @@ __global__ __launch_bounds__(kTs) void topk_split_kernel(const TopkArgs a) {
 // Slices per row of the split path (1: one CTA per row).  At most ~3 split CTAs fit a CU.
 int split_count(int64_t rows, int64_t width, int max_splits, int n_cu) {
   if (rows <= 0 || rows > kTs) return 1;  // the balanced split assigns one row per thread
-  int64_t s = (width + 8191) / 8192;  // splitting rows of <= 8192 tokens does not pay
+  // one CTA streams a row of up to ~32K tokens faster than a split pays for its publication
+  // round trip (measured on 32 x 16K and 64 x U[2K, 64K] decode batches)
+  int64_t s = width > 32768 ? (width + 16383) / 16384 : 1;
   s = s < 1 ? 1 : s;
   const int64_t by_cu = (3 * static_cast<int64_t>(n_cu)) / rows;
   s = s < by_cu ? s : by_cu;
