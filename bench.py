@@ -5,8 +5,10 @@ A step is one pass of the indexer over one batch with every input resident in HB
            page-table remap
   prefill  paged K dequant to bf16 -> q quant -> causal fp8 MQA logits -> top-2048 + remap
 Steps are captured in a hipGraph (--steps-per-graph of them per graph, as a serving loop
-captures the indexer inside its model step) and replayed; W steps warm up, exactly K steps are
-timed between two synchronisations.  value = indexer K-tokens scored per second (tokens scored =
+captures the indexer inside its model step) and replayed.  The step graph first runs untimed
+for --settle-ms (the GPU raises its clocks only after some milliseconds of load; a serving loop
+runs continuously), then W more steps warm up, then exactly K steps are timed between two
+synchronisations.  value = indexer K-tokens scored per second (tokens scored =
 sum over query rows of the keys that row scores).
 
 The JSON line also carries
@@ -265,9 +267,20 @@ def graph_of(fn, torch, n=1):
     return g
 
 
-def kernel_time_ms(fn, torch, reps=20, rounds=5):
-    """Average duration of fn's launch: a graph of `reps` back-to-back launches, replayed and
-    timed with HIP events on the current stream; median over rounds."""
+def settle(g, torch, ms):
+    """Replays graph g untimed for about `ms` milliseconds of GPU time."""
+    if ms <= 0:
+        return
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            g.replay()
+        torch.cuda.synchronize()
+
+
+def kernel_time_ms(fn, torch, reps=20, rounds=5, settle_ms=50.0):
+    """Average duration of fn's launch: a graph of `reps` back-to-back launches, replayed untimed
+    for settle_ms, then timed with HIP events on the current stream; median over rounds."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -278,9 +291,10 @@ def kernel_time_ms(fn, torch, reps=20, rounds=5):
     with torch.cuda.graph(g):
         for _ in range(reps):
             fn()
-    for _ in range(3):  # first replays of a new graph run slow (fresh buffers, clocks)
+    for _ in range(3):  # first replays of a new graph run slow (fresh buffers)
         g.replay()
     torch.cuda.synchronize()
+    settle(g, torch, settle_ms)
     times = []
     for _ in range(rounds):
         a = torch.cuda.Event(enable_timing=True)
@@ -298,7 +312,9 @@ def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20, help="untimed steps right before the timed ones")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed replays of the step graph first, so that the GPU clocks have settled")
     ap.add_argument("--workload", default="decode_mtp64", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -337,11 +353,14 @@ def main(argv=None):
     # timed region runs exactly K steps (full graphs, then single-step graphs for the rest).
     per = max(1, min(args.steps_per_graph, args.steps))
     g = graph_of(step, torch, per)
-    g1 = graph_of(step, torch, 1) if args.steps % per else None
-    for _ in range(args.warmup):
-        g1.replay() if g1 is not None else g.replay()
+    g1 = graph_of(step, torch, 1) if args.steps % per or args.warmup % per else None
+    settle(g, torch, args.settle_ms)
+    for _ in range(args.warmup // per):
+        g.replay()
+    for _ in range(args.warmup % per):
+        g1.replay()
     torch.cuda.synchronize()
-    log(f"warmup done ({args.warmup} graph replays)")
+    log(f"warmup done ({args.settle_ms:.0f} ms of step replays, then {args.warmup} steps)")
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -401,7 +420,8 @@ def main(argv=None):
         "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)", "data": "synthetic (seeded, see workloads.py)",
         "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "query_rows": int(case.rows),
                    "tokens_scored_per_step": int(tokens),
-                   "graph": f"hipGraph of {per} steps per replay"},
+                   "graph": f"hipGraph of {per} steps per replay",
+                   "settle_ms": args.settle_ms},
         "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -150,71 +150,12 @@ __device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
   return before + inc - x;
 }
 
-// Launch shape per (rows per CTA R, fused histogram): S page streams per CTA with NS LDS slots
-// each, and the block-table slice a CTA stages (the host keeps P / T within it; it also bounds a
-// row's tokens per CTA below 2^16 for the 16-bit histogram counters).  Measured on the 64-request
-// MTP decode: one stream per CTA (eight CTAs per CU) without the histogram; with it, the 8 KB
-// per row of counters is amortised over two streams (R = 2) or four (R = 1).
-template <int R, bool kHist>
-struct Shape {
-  static constexpr int S = kHist ? (R == 1 ? 4 : (R == 2 ? 2 : 1)) : 1;
-  static constexpr int NS = 2;
-  static constexpr int kMaxPages = S == 1 ? 255 : (S == 2 ? 511 : 1023);
-  static constexpr int kLds = S * NS * kPageBytes + (kHist ? R * kBins * 2 : 0) + kMaxPages * 4 + 512;
-  static constexpr int kByLds = kLdsBytes / kLds;
-  static constexpr int kByWaves = kMaxWavesCu / (R * S) > 0 ? kMaxWavesCu / (R * S) : 1;
-  static constexpr int kCtasPerCu = kByLds < kByWaves ? kByLds : kByWaves;
-  static constexpr int kThreads = R * S * kWave;
-  static constexpr int kWavesPerSimd = (kCtasPerCu * R * S + 3) / 4;
-};
-
-// VMEM ops of wave r's share of a page DMA (blocks r, r + R, ... of 8; the last wave adds the
-// scales).
-template <int R>
-__device__ __forceinline__ int dma_ops(int r) { return (8 - r + R - 1) / R + (r == R - 1 ? 1 : 0); }
-
-// s_waitcnt vmcnt(n) for a wave-uniform n in 0..15 (gfx9 encoding; expcnt / lgkmcnt not waited).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-  }
-}
-
-
-
-template <int H, int R, bool kHist>
-__global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_waves_per_eu(
-    Shape<R, kHist>::kWavesPerSimd))) void mqa_logits_decode_kernel(const DecodeArgs a) {
-  constexpr int HT = H / 16;  // head tiles
-  using Sh = Shape<R, kHist>;
-  constexpr int S = Sh::S;
-  constexpr int NS = Sh::NS;
-  static_assert(NS == 2 || NS == 3, "2 or 3 page slots per stream");
-  constexpr int NT = Sh::kThreads;
-  __shared__ __attribute__((aligned(16))) uint8_t s_slot0[S][kPageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t s_slot1[S][kPageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t s_slot2[NS > 2 ? S : 1][NS > 2 ? kPageBytes : 16];
-  __shared__ uint32_t s_hist[kHist ? R * kBins / 2 : 1];  // 16-bit counters, two bins per word
-  __shared__ int s_cnt[2 * R];
-  __shared__ int s_w[2][NT / kWave];
-  __shared__ int s_assign[3];  // group, index within the group's CTAs, the group's CTA count
-  __shared__ int s_bt[Sh::kMaxPages];
-
+// Work assignment, identical in every CTA: s_assign = {group (-1: none), index among the group's
+// CTAs, their count}; group g gets ceil(pages_g * T / P) CTAs.  Ends before a barrier (the caller's).
+template <int NT>
+__device__ void assign_cta(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* s_assign) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
   const int cta = blockIdx.x;
-
-  // ---- work assignment (identical in every CTA) ----
   // Thread tid owns groups [g_lo, g_hi); their page counts are read once and kept (up to kGpt
   // a thread, else re-read).
   constexpr int kGpt = 4;
@@ -265,6 +206,71 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
       c0 += n;
     }
   }
+}
+
+// Launch shape per (rows per CTA R, fused histogram): S page streams per CTA with NS LDS slots
+// each, and the block-table slice a CTA stages (the host keeps P / T within it; it also bounds a
+// row's tokens per CTA below 2^16 for the 16-bit histogram counters).  Measured on the 64-request
+// MTP decode: one stream per CTA (eight CTAs per CU) without the histogram; with it, the 8 KB
+// per row of counters is amortised over two streams (R = 2) or four (R = 1).
+template <int R, bool kHist>
+struct Shape {
+  static constexpr int S = kHist ? (R == 1 ? 4 : (R == 2 ? 2 : 1)) : 1;
+  static constexpr int NS = 2;
+  static constexpr int kMaxPages = S == 1 ? 255 : (S == 2 ? 511 : 1023);
+  static constexpr int kLds = S * NS * kPageBytes + (kHist ? R * kBins * 2 : 0) + kMaxPages * 4 + 512;
+  static constexpr int kByLds = kLdsBytes / kLds;
+  static constexpr int kByWaves = kMaxWavesCu / (R * S) > 0 ? kMaxWavesCu / (R * S) : 1;
+  static constexpr int kCtasPerCu = kByLds < kByWaves ? kByLds : kByWaves;
+  static constexpr int kThreads = R * S * kWave;
+  static constexpr int kWavesPerSimd = (kCtasPerCu * R * S + 3) / 4;
+};
+
+// VMEM ops of wave r's share of a page DMA (blocks r, r + R, ... of 8; the last wave adds the
+// scales).
+template <int R>
+__device__ __forceinline__ int dma_ops(int r) { return (8 - r + R - 1) / R + (r == R - 1 ? 1 : 0); }
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in 0..15 (gfx9 encoding; expcnt / lgkmcnt not waited).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+  }
+}
+
+template <int H, int R, bool kHist>
+__global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_waves_per_eu(
+    Shape<R, kHist>::kWavesPerSimd))) void mqa_logits_decode_kernel(const DecodeArgs a) {
+  constexpr int HT = H / 16;  // head tiles
+  using Sh = Shape<R, kHist>;
+  constexpr int S = Sh::S;
+  constexpr int NS = Sh::NS;
+  static_assert(NS == 2 || NS == 3, "2 or 3 page slots per stream");
+  constexpr int NT = Sh::kThreads;
+  __shared__ __attribute__((aligned(16))) uint8_t s_slot0[S][kPageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_slot1[S][kPageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_slot2[NS > 2 ? S : 1][NS > 2 ? kPageBytes : 16];
+  __shared__ uint32_t s_hist[kHist ? R * kBins / 2 : 1];  // 16-bit counters, two bins per word
+  __shared__ int s_cnt[2 * R];
+  __shared__ int s_w[2][NT / kWave];
+  __shared__ int s_assign[3];  // group, index within the group's CTAs, the group's CTA count
+  __shared__ int s_bt[Sh::kMaxPages];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int cta = blockIdx.x;
+
+  assign_cta<NT>(a, s_w, s_assign);
 
   // The paired top-k's per-row counters (words 0..2 of each row of the workspace's second
   // block [histograms rows*4096 | counters rows*4096 | counts rows*2]), a row per CTA; issued
