@@ -40,21 +40,19 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
 // fp32 -> OCP fp8 e4m3fn (bias 7, max 448, no infinities), round to nearest even, not
 // saturating: |x| > 464 (which rounds past 448; 464 itself ties to the even 448), infinities and
 // NaN give 0x7F | sign -- the behaviour of torch's float -> float8_e4m3fn cast.  Written from
-// the format definition.
+// the format definition with no select or branch (a converted select becomes a branch per
+// value, and many conversions in a row then spill): on a = |x| clamped to [2^-6, inf), the
+// normal code (3 mantissa bits kept, RNE on the other 20; >= 0x7F past 448, capped there) plus
+// the subnormal code of min(a, 2^-6) (RNE on the grid of 2^-9: 8 at 2^-6) minus 8.
 __device__ __forceinline__ uint32_t fp8_e4m3_rne(float x) {
   const uint32_t u = __float_as_uint(x);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7FFFFFFFu;
-  uint32_t code;
-  if (a > 0x43E80000u) {                  // above 464.0f, +inf, NaN
-    code = 0x7Fu;
-  } else if (a < 0x3C800000u) {           // below 2^-6: subnormal grid of 2^-9
-    code = static_cast<uint32_t>(rintf(__uint_as_float(a) * 512.0f));
-  } else {                                // normal: keep 3 mantissa bits, RNE on the other 20
-    const uint32_t t = a + 0x7FFFFu + ((a >> 20) & 1u);
-    code = (t >> 20) - (120u << 3);
-  }
-  return code | sign;
+  const uint32_t lo = min(a, 0x3C800000u);
+  const uint32_t hi = max(a, 0x3C800000u);
+  const uint32_t sub = static_cast<uint32_t>(rintf(__uint_as_float(lo) * 512.0f));
+  const uint32_t nrm = min(((hi + 0x7FFFFu + ((hi >> 20) & 1u)) >> 20) - (120u << 3), 0x7Fu);
+  return (nrm + sub - 8u) | sign;
 }
 
 // OCP fp8 e4m3fn -> fp32, exact (software; used where the throughput does not matter).
@@ -66,6 +64,14 @@ __device__ __forceinline__ float fp8_e4m3_to_f32(uint32_t b) {
   else if (e == 15 && m == 7) v = __uint_as_float(0x7FC00000u);
   else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
   return (b & 0x80u) ? -v : v;
+}
+
+// Factors of the per-vector fp8 quantisation (hcu_ops/csrc/norm_quant.cu:13-14): for
+// amax = max|x| over the vector, the codes are fp8_e4m3_rne(x * inv) with inv = 448 / amax
+// (0 when amax == 0) and the dequantisation scale is amax / 448.
+__device__ __forceinline__ void quant_factors(float amax, float& inv, float& scale) {
+  inv = amax == 0.0f ? 0.0f : 448.0f / amax;
+  scale = amax / 448.0f;
 }
 
 // ------------------------------------------------------------------------------------------

@@ -312,8 +312,14 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   const int n_local = p_end - p_begin;  // <= Sh::kMaxPages by the host's choice of target
   const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride + p_begin;
 
-  // the first page of every stream in flight first, straight from the block table
-  if (s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[s]) * a.page_stride, s_slot0[s], r, lane);
+  // The block-table entries of the stream's first two pages, read together and waited for
+  // here: the second page's DMA then needs no wait (one later would also wait for the first
+  // page, every VMEM operation before it counting).  Then the first page of every stream.
+  int bt_first = 0, bt_second = 0;
+  if (s < n_local) bt_first = btr[s];
+  if (S + s < n_local) bt_second = btr[S + s];
+  wait_vmcnt(0);
+  if (s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(bt_first) * a.page_stride, s_slot0[s], r, lane);
 
   // q / w fragments of this wave's row: lane l holds head ht*16 + l%16, bytes (l/16)*32 .. +32,
   // and the weights of heads ht*16 + 4*(l/16) + e, the rows of the MFMA result it holds.
@@ -338,7 +344,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   // is needed here.
   for (int b = wave * kWave; b < n_local; b += NT)
     if (b + lane < n_local) __builtin_amdgcn_global_load_lds(btr + b + lane, &s_bt[b], 4, 0, 0);
-  if (S + s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(btr[S + s]) * a.page_stride, s_slot1[s], r, lane);
+  if (S + s < n_local) dma_page<R>(a.kv + static_cast<int64_t>(bt_second) * a.page_stride, s_slot1[s], r, lane);
   if constexpr (kHist) {
     for (int i = tid; i < R * kBins / 2; i += NT) s_hist[i] = 0;
     if (tid < 2 * R) s_cnt[tid] = 0;

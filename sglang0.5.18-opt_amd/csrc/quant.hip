@@ -29,8 +29,8 @@ __device__ __forceinline__ float quant_vec(const uint16_t* src, int sub, u32x2& 
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
 #pragma unroll
   for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  const float inv = amax == 0.0f ? 0.0f : 448.0f / amax;
-  scale = amax / 448.0f;
+  float inv;
+  quant_factors(amax, inv, scale);
   uint32_t c[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) c[i] = fp8_e4m3_rne(x[i] * inv);
