@@ -77,12 +77,15 @@ template <int R>
 __device__ __forceinline__ void dma_page(const uint8_t* page, uint8_t* slot, int r, int lane) {
 #pragma unroll
   for (int j = r; j < 8; j += R) {
-    const int c = j * 64 + lane;
-    const int t = c >> 3;
-    const int p = (c & 7) ^ ((t >> 1) & 7);
-    __builtin_amdgcn_global_load_lds(page + t * kHeadDim + p * 16, slot + j * 1024, 16, 0, 0);
+    const uint32_t c = j * 64 + lane;
+    const uint32_t t = c >> 3;
+    const uint32_t p = (c & 7) ^ ((t >> 1) & 7);
+    // unsigned 32-bit lane offsets: a wave-uniform page pointer then serves as the scalar base
+    __builtin_amdgcn_global_load_lds(page + (t * kHeadDim + p * 16), slot + j * 1024, 16, 0, 0);
   }
-  if (r == R - 1) __builtin_amdgcn_global_load_lds(page + kPageFp8Bytes + lane * 4, slot + kPageFp8Bytes, 4, 0, 0);
+  if (r == R - 1)
+    __builtin_amdgcn_global_load_lds(page + static_cast<uint32_t>(kPageFp8Bytes + lane * 4), slot + kPageFp8Bytes, 4,
+                                     0, 0);
 }
 
 // 32 bytes (chunks p0, p0 + 1) of token t from a slot, as an MFMA operand.
@@ -415,8 +418,12 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     flush();
-    if (i + (NS - 1) * S < n_local && (NS > 2 || k > 0))  // NS = 2: page S + s came with the prologue
-      dma_page<R>(a.kv + static_cast<int64_t>(s_bt[i + (NS - 1) * S]) * a.page_stride, nxt, r, lane);
+    if (i + (NS - 1) * S < n_local && (NS > 2 || k > 0)) {  // NS = 2: page S + s came with the prologue
+      // the entry is the same in every lane: as a scalar, the page address is scalar arithmetic
+      // and the DMA takes it as its scalar base (no 64-bit per-lane address math)
+      const int pg = __builtin_amdgcn_readfirstlane(s_bt[i + (NS - 1) * S]);
+      dma_page<R>(a.kv + static_cast<int64_t>(pg) * a.page_stride, nxt, r, lane);
+    }
     if (i >= n_local) return;  // stream-uniform (the stream still takes part in the barriers)
     const float scale = reinterpret_cast<const float*>(cur + kPageFp8Bytes)[lane];
     float part[4];  // this lane's heads' share of tokens st * 16 + lane % 16
@@ -439,7 +446,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     const float v = val * scale;
     pend_p = p;
     pend_v = v;
-    pend_bits = __ballot(p * kPage + lane < len && __float_as_uint(v) != 0u);
+    pend_bits = (a.mask != nullptr || kHist) ? __ballot(p * kPage + lane < len && __float_as_uint(v) != 0u) : 0;
   };
   // the two slots of a stream are distinct LDS objects, so the compiler can tell that the
   // reads of one do not wait for the DMA into the other
