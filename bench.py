@@ -196,7 +196,7 @@ class PrefillStep:
             r1 = min(r0 + self.slab, self.case.rows)
             lg = h.mqa_logits_prefill(q8[r0:r1], w[r0:r1], self.kv, self.bt, self.lens[r0:r1], self.width)
             cu = self.cu if r1 - r0 == self.slab else self.cu_tail
-            self.out[r0:r1] = h.topk_transform(lg, self.lens[r0:r1], self.pt, cu)
+            h.topk_transform(lg, self.lens[r0:r1], self.pt, cu, out=self.out[r0:r1])
         return self.out
 
     def logits_only(self):

@@ -115,7 +115,7 @@ void check_topk(const torch::Tensor& score, const c10::optional<torch::Tensor>& 
 torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::Tensor>& nonzero_mask,
                         const torch::Tensor& lengths, const torch::Tensor& page_table_size_1,
                         const torch::Tensor& cu_seqlens_q, int64_t topk, int64_t max_splits,
-                        const torch::Tensor* zws, bool pass1_done) {
+                        const torch::Tensor* zws, bool pass1_done, const torch::Tensor* out = nullptr) {
   check_topk(score, nonzero_mask, lengths, page_table_size_1, topk);
   const int64_t rows = score.size(0);
   const int64_t width = score.size(1);
@@ -128,7 +128,15 @@ torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::T
                 "varlen layout needs int32 cu_seqlens_q [requests + 1] with one page-table row per request");
   }
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(score.device());
-  auto dst = torch::empty({rows, kTopK}, score.options().dtype(at::kInt));
+  torch::Tensor dst;
+  if (out != nullptr) {
+    TORCH_CHECK(out->is_cuda() && out->scalar_type() == at::kInt && out->dim() == 2 && out->size(0) == rows &&
+                    out->size(1) == kTopK && out->is_contiguous(),
+                "out must be a contiguous int32 [rows, 2048] tensor");
+    dst = *out;
+  } else {
+    dst = torch::empty({rows, kTopK}, score.options().dtype(at::kInt));
+  }
   if (rows == 0) return dst;
   const int cus = n_cu();
   const int splits = static_cast<int>(std::max<int64_t>(1, max_splits));
@@ -183,8 +191,9 @@ torch::Tensor sparse_mask_topk_transform_split_pre(const torch::Tensor& score, c
 // Dense-score top-k (no sparse mask: every score below the row length is valid), e.g. prefill.
 torch::Tensor topk_transform(const torch::Tensor& score, const torch::Tensor& lengths,
                              const torch::Tensor& page_table_size_1, const torch::Tensor& cu_seqlens_q,
-                             int64_t topk, int64_t max_splits) {
-  return topk_impl(score, c10::nullopt, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, nullptr, false);
+                             int64_t topk, int64_t max_splits, const c10::optional<torch::Tensor>& out) {
+  return topk_impl(score, c10::nullopt, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, nullptr, false,
+                   out.has_value() ? &*out : nullptr);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -308,7 +317,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("score"), py::arg("nonzero_mask"), py::arg("lengths"), py::arg("page_table_size_1"),
         py::arg("cu_seqlens_q"), py::arg("topk"), py::arg("max_splits"), py::arg("zws"),
         py::arg("pass1_done") = false);
-  m.def("topk_transform", &topk_transform, "Exact top-2048 + page-table transform over dense scores");
+  m.def("topk_transform", &topk_transform, "Exact top-2048 + page-table transform over dense scores (into out if given)",
+        py::arg("score"), py::arg("lengths"), py::arg("page_table_size_1"), py::arg("cu_seqlens_q"), py::arg("topk"),
+        py::arg("max_splits"), py::arg("out") = py::none());
   m.def("dequant_k_paged", &dequant_k_paged, "indexer 132-B paged fp8 K -> bf16 [n, 128]");
   m.def("gather_k_paged", &gather_k_paged, "indexer 132-B paged fp8 K -> contiguous (fp8 [n, 128], f32 [n])");
   m.def("dequantize_k_cache_paged", &dequantize_k_cache_paged, "MLA 656-B paged fp8 slot -> bf16 [n, 1, 576]");

@@ -133,9 +133,10 @@ def mqa_logits_prefill(q, weights, kv_cache, block_table, lens, width):
     return _C.mqa_logits_prefill(q, weights, kv_cache, block_table, lens, width)
 
 
-def topk_transform(score, lengths, page_table_size_1, cu_seqlens_q, topk=2048, max_splits=None):
+def topk_transform(score, lengths, page_table_size_1, cu_seqlens_q, topk=2048, max_splits=None, out=None):
     """Top-2048 + page-table transform over dense scores (every score below the length valid);
-    cu_seqlens_q [requests + 1] maps rows to their request's page-table row (varlen layout)."""
+    cu_seqlens_q [requests + 1] maps rows to their request's page-table row (varlen layout).
+    out: an int32 [rows, 2048] contiguous tensor to write (and return) instead of a new one."""
     if max_splits is None:
         max_splits = _TOPK_SPLITS if _TOPK_IMPL == "split" else 1
-    return _C.topk_transform(score, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits)
+    return _C.topk_transform(score, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, out)

@@ -145,3 +145,9 @@ def test_topk_sampled_threshold_fallback(gpu, pattern):
         assert np.array_equal(got, ref), f"{pattern} impl={name}"
     got = hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1)
     assert np.array_equal(sorted_rows(got.cpu().numpy()), ref), f"{pattern} dense"
+    # into a caller's buffer: rows 1.. of a larger output, the other rows untouched
+    buf = torch.full((B + 1, 2048), -7, dtype=torch.int32, device=gpu)
+    ret = hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1, out=buf[1:])
+    assert ret.data_ptr() == buf[1:].data_ptr()
+    assert np.array_equal(sorted_rows(buf[1:].cpu().numpy()), ref), f"{pattern} dense into out"
+    assert (buf[0] == -7).all()
