@@ -74,6 +74,33 @@ __device__ __forceinline__ void quant_factors(float amax, float& inv, float& sca
   scale = amax / 448.0f;
 }
 
+// One 128-element bf16 vector quantised by 16 lanes (lane `sub` holds elements 8 sub .. 8 sub + 7;
+// the 16 lanes are 16 consecutive lanes of the wave, aligned to 16): the vector's amax (all 16
+// lanes agree), its dequantisation scale and this lane's 8 fp8 codes packed in two words.
+__device__ __forceinline__ float quant_vec16(const uint16_t* src, int sub, uint32_t& lo, uint32_t& hi, float& scale) {
+  const uint4 raw = *reinterpret_cast<const uint4*>(src + sub * 8);
+  const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(r[i] << 16);
+    x[2 * i + 1] = __uint_as_float(r[i] & 0xFFFF0000u);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  float inv;
+  quant_factors(amax, inv, scale);
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = fp8_e4m3_rne(x[i] * inv);
+  lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+  hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  return amax;
+}
+
 // ------------------------------------------------------------------------------------------
 // Wave helpers (wave64).
 __device__ __forceinline__ int lane_id() { return static_cast<int>(__lane_id()); }

@@ -8,33 +8,16 @@
 namespace dsa {
 namespace {
 
-using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
 
 constexpr int kQThreads = 256;
 constexpr int kVecPerCta = kQThreads / 16;
 
-// Loads this lane's 8 bf16 of a vector, returns the vector's amax (all 16 lanes agree) and
-// the 8 fp8 codes packed into two words.
+// quant_vec16 (dsa_common.h) with the two code words as one 8-B store.
 __device__ __forceinline__ float quant_vec(const uint16_t* src, int sub, u32x2& packed, float& scale) {
-  const u32x4 raw = *reinterpret_cast<const u32x4*>(src + sub * 8);
-  float x[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = __uint_as_float(raw[i] << 16);
-    x[2 * i + 1] = __uint_as_float(raw[i] & 0xFFFF0000u);
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  float inv;
-  quant_factors(amax, inv, scale);
-  uint32_t c[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) c[i] = fp8_e4m3_rne(x[i] * inv);
-  packed = u32x2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24), c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
+  uint32_t lo, hi;
+  const float amax = quant_vec16(src, sub, lo, hi, scale);
+  packed = u32x2{lo, hi};
   return amax;
 }
 
