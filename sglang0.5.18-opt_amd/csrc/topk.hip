@@ -1226,8 +1226,18 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
   __shared__ SampledLds L;
   constexpr int kStep = kTs * 4 * kUnroll;
   const int tid = threadIdx.x;
-  const int row = blockIdx.x / a.S;
-  const int slice = blockIdx.x - row * a.S;
+  // The S CTAs of a row on one XCD when the rows fill whole octets (CTAs are spread over the 8
+  // XCDs by blockIdx % 8): the row's sample is then fetched from HBM once, the other CTAs hit
+  // that XCD's L2.
+  int row, slice;
+  if ((a.rows & 7) == 0) {
+    const int l = static_cast<int>(blockIdx.x) >> 3;
+    row = ((l / a.S) << 3) | (static_cast<int>(blockIdx.x) & 7);
+    slice = l % a.S;
+  } else {
+    row = blockIdx.x / a.S;
+    slice = blockIdx.x - row * a.S;
+  }
   const int len = row_len(a, row);
   if (len <= kTopK) {
     if (slice == 0) copy_short_row<kTs>(pt_row(a, row), a.out + static_cast<int64_t>(row) * kTopK, len);
