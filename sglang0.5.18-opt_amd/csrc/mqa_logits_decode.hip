@@ -270,7 +270,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: row pointers become scalar
   const int cta = blockIdx.x;
 
   assign_cta<NT>(a, s_w, s_assign);
@@ -384,13 +384,17 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   int pend_p = -1;  // page of the held results (wave-uniform), -1: none
   float pend_v = 0.0f;
   uint64_t pend_bits = 0;
+  // the row's logits / mask rows as scalar bases, the token as an unsigned 32-bit lane offset:
+  // each store is the scalar-base form, no 64-bit address arithmetic per lane
+  float* const lrow = a.logits + static_cast<int64_t>(row) * a.logits_stride;
+  int16_t* const mrow = a.mask + static_cast<int64_t>(row) * a.mask_stride;
   auto flush = [&]() {
     if (pend_p < 0) return;
     const int token = pend_p * kPage + lane;
     if (a.mask != nullptr && lane < 4)
-      a.mask[static_cast<int64_t>(row) * a.mask_stride + pend_p * 4 + lane] =
+      *reinterpret_cast<int16_t*>(reinterpret_cast<char*>(mrow) + static_cast<uint32_t>((pend_p * 4 + lane) * 2)) =
           static_cast<int16_t>((pend_bits >> (16 * lane)) & 0xFFFFu);
-    if (token < len) a.logits[static_cast<int64_t>(row) * a.logits_stride + token] = pend_v;
+    if (token < len) *reinterpret_cast<float*>(reinterpret_cast<char*>(lrow) + static_cast<uint32_t>(token * 4)) = pend_v;
     if constexpr (kHist) {
       if (((pend_bits >> lane) & 1u) && token < hlim) {
         const uint32_t key = float_key(pend_v);
