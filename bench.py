@@ -46,7 +46,11 @@ WORKLOADS = {
                       "64 heads x 128",
     "prefill_16k_128k": "long prefill, 16384 query rows over 147456 keys (causal) in 4096-row slabs, "
                         "Student-t(4) K, 64 heads x 128",
+    "dequant_mla_393k": "MLA K-cache dequant, 392832 tokens gathered at random from 2^19 656-B slots -> bf16 [n, 576]",
+    "dequant_mla_131k": "MLA K-cache dequant, 131072 tokens gathered at random from 2^19 656-B slots -> bf16 [n, 576]",
+    "dequant_k_74k": "indexer K dequant, the 73728 keys of prefill_8k_64k from the 132-B paged cache -> bf16 [n, 128]",
 }
+DEQUANT_METRIC = "paged K-cache dequant, algorithmic GB/s (slot index + slot bytes read, bf16 written)"
 
 
 def profiled_traffic(kernel, workload):
@@ -249,6 +253,46 @@ def prefill_cpu_baseline(case, budget_s):
 
 
 # ---------------------------------------------------------------------------------------------
+# Dequant (the prefill path's gather of K to bf16, and the MLA cache's)
+
+class DequantStep:
+    def __init__(self, case, dev):
+        import hcu_ops
+        self.h = hcu_ops
+        self.case = case
+        self.mla = hasattr(case, "cache")
+        self.src = (case.cache if self.mla else case.kv).to(dev)
+        self.slots = case.slots.to(dev)
+        self.kernel = "dequant_mla_kernel" if self.mla else "dequant_k_kernel"
+        # per token: slot index + the slot's bytes read, bf16 row written
+        self.tok_bytes = 4 + (656 + 576 * 2 if self.mla else 132 + 128 * 2)
+
+    def __call__(self):
+        if self.mla:
+            return self.h.dequantize_k_cache_paged(self.src, self.slots)
+        return self.h.dequant_k_paged(self.src, self.slots)
+
+    def bytes(self):
+        return self.case.tokens * self.tok_bytes
+
+
+def dequant_cpu_baseline(case, budget_s, tok_bytes):
+    """The oracle's numpy dequant over consecutive chunks of the slot list until budget_s."""
+    from oracle import indexer as O
+    mla = hasattr(case, "cache")
+    src = (case.cache.view(case.cache.shape[0], -1) if mla else case.kv.view(case.kv.shape[0], -1)).numpy()
+    slots = case.slots.numpy()
+    done = 0
+    t0 = time.perf_counter()
+    while done < slots.shape[0] and time.perf_counter() - t0 < budget_s:
+        s = slots[done:done + 8192]
+        O.dequant_mla(src, s) if mla else O.dequant_k_paged(src, s)
+        done += s.shape[0]
+    dt = time.perf_counter() - t0
+    return done * tok_bytes / dt / 1e9, f"{done} of {slots.shape[0]} tokens in {dt:.1f} s (numpy, one thread)"
+
+
+# ---------------------------------------------------------------------------------------------
 
 def graph_of(fn, torch, n=1):
     """hipGraph of n back-to-back calls of fn (after two eager warm-up calls)."""
@@ -345,7 +389,8 @@ def main(argv=None):
     case = getattr(wl, args.workload)()
     log(f"built {args.workload} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
     decode = args.workload.startswith("decode")
-    step = DecodeStep(case, dev) if decode else PrefillStep(case, dev)
+    dequant = args.workload.startswith("dequant")
+    step = DecodeStep(case, dev) if decode else (DequantStep(case, dev) if dequant else PrefillStep(case, dev))
     torch.cuda.synchronize()
 
     # Steps are captured `steps_per_graph` to a hipGraph, as a serving loop captures the indexer
@@ -372,6 +417,8 @@ def main(argv=None):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
+    if dequant:
+        return dequant_report(args, case, step, ms, per, torch)
     tokens = step.tokens()
     value = tokens / 1e3 / (ms / 1e3)
     log(f"timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
@@ -423,6 +470,35 @@ def main(argv=None):
                    "graph": f"hipGraph of {per} steps per replay",
                    "settle_ms": args.settle_ms},
         "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def dequant_report(args, case, step, ms, per, torch):
+    """The JSON line of a dequant workload: a step is one dequant launch."""
+    nb = step.bytes()
+    value = nb / (ms / 1e3) / 1e9
+    k_ms = kernel_time_ms(step, torch)
+    achieved = nb / (k_ms / 1e3) / 1e9
+    log(f"timed {args.steps} launches: {ms * 1e3:.1f} us each, {value:.1f} GB/s; graph of 20 alone {k_ms * 1e3:.1f} us")
+    traffic, tsrc = profiled_traffic(step.kernel, args.workload)
+    roofline = {"bound": "hbm", "kernel": step.kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": tsrc,
+                "algorithmic_bytes": nb, "kernel_us": round(k_ms * 1e3, 2)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        v, sample = dequant_cpu_baseline(case, args.cpu_budget, step.tok_bytes)
+        cpu = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port", "sample": sample, "cpu": cpu_model()}
+        log(f"cpu baseline {v:.3g} GB/s ({sample})")
+    line = {
+        "metric": DEQUANT_METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8e4m3 -> bf16", "data": "synthetic (seeded, see workloads.py)",
+        "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "tokens": int(case.tokens),
+                   "bytes_per_token": step.tok_bytes, "graph": f"hipGraph of {per} launches per replay",
+                   "settle_ms": args.settle_ms},
+        "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0

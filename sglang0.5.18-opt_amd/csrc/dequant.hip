@@ -85,41 +85,65 @@ constexpr int kMlaNope = 512;
 constexpr int kMlaScaleOff = 512;
 constexpr int kMlaRopeOff = 528;
 constexpr int kMlaItems = 40;
+constexpr int kMlaUnroll = 4;  // work items per thread per pass, their loads issued together
 
+// I: the index type (uint32_t when n * 40 fits, else int64_t).  Each pass takes kMlaUnroll items
+// a grid apart: their slot indices, then their slot bytes, are loaded before any is used, so a
+// thread keeps kMlaUnroll 16-B loads in flight (one dependent slot -> bytes chain per pass).
+template <typename I>
 __global__ __launch_bounds__(kDqThreads) void dequant_mla_kernel(
     const uint8_t* __restrict__ cache, int64_t stride, const int32_t* __restrict__ slots,
     int64_t n, uint16_t* __restrict__ out, int64_t out_stride) {
-  const int64_t total = n * kMlaItems;
-  for (int64_t g = static_cast<int64_t>(blockIdx.x) * kDqThreads + threadIdx.x; g < total;
-       g += static_cast<int64_t>(gridDim.x) * kDqThreads) {
-    const int64_t tok = g / kMlaItems;
-    const int c = static_cast<int>(g - tok * kMlaItems);
-    const int32_t slot = slots[tok];
-    const uint8_t* src = cache + static_cast<int64_t>(slot < 0 ? 0 : slot) * stride;
-    uint16_t* dst = out + tok * out_stride;
-    if (c < 32) {
-      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-      if (slot >= 0) {
-        const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + c * 16));
-        const float s = *reinterpret_cast<const float*>(src + kMlaScaleOff + (c >> 3) * 4);
-        dequant16(q, s, lo, hi);
+  constexpr int U = kMlaUnroll;
+  const I total = static_cast<I>(n * kMlaItems);
+  const I step = static_cast<I>(gridDim.x) * kDqThreads;
+  for (I g0 = static_cast<I>(blockIdx.x) * kDqThreads + threadIdx.x; g0 < total; g0 += step * U) {
+    I tok[U];
+    int c[U];
+    int32_t slot[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const I g = g0 + u * step;
+      const bool in = g < total;
+      tok[u] = in ? g / kMlaItems : 0;
+      c[u] = static_cast<int>(g - tok[u] * kMlaItems);
+      slot[u] = in ? slots[tok[u]] : -1;
+    }
+    u32x4 v[U];
+    float s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      s[u] = 0.0f;
+      if (slot[u] >= 0) {
+        const uint8_t* src = cache + static_cast<int64_t>(slot[u]) * stride;
+        const bool nope = c[u] < 32;
+        v[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(src + (nope ? c[u] * 16 : kMlaRopeOff + (c[u] - 32) * 16)));
+        if (nope) s[u] = *reinterpret_cast<const float*>(src + kMlaScaleOff + (c[u] >> 3) * 4);
       }
-      u32x4* o = reinterpret_cast<u32x4*>(dst + c * 16);
-      o[0] = lo;
-      o[1] = hi;
-    } else {
-      const int rc = c - 32;
-      u32x4 r = {0u, 0u, 0u, 0u};
-      if (slot >= 0) r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + kMlaRopeOff + rc * 16));
-      *reinterpret_cast<u32x4*>(dst + kMlaNope + rc * 8) = r;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (g0 + u * step >= total) break;
+      uint16_t* dst = out + static_cast<int64_t>(tok[u]) * out_stride;
+      if (c[u] < 32) {
+        u32x4 lo, hi;
+        dequant16(v[u], s[u], lo, hi);
+        u32x4* o = reinterpret_cast<u32x4*>(dst + c[u] * 16);
+        o[0] = lo;
+        o[1] = hi;
+      } else {
+        *reinterpret_cast<u32x4*>(dst + kMlaNope + (c[u] - 32) * 8) = v[u];
+      }
     }
   }
 }
 
-int grid_for(int64_t work_items) {
+int grid_for(int64_t work_items, int64_t cap = 8192) {
   // Enough CTAs to cover the 256 CUs several times; the kernels grid-stride over the rest.
   const int64_t want = (work_items + kDqThreads - 1) / kDqThreads;
-  return static_cast<int>(want < 8192 ? (want > 0 ? want : 1) : 8192);
+  return static_cast<int>(want < cap ? (want > 0 ? want : 1) : cap);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -169,7 +193,15 @@ extern "C" int dsa_dequant_mla_paged(const uint8_t* cache, int64_t cache_stride_
               "dsa_dequant_mla_paged: slots must be >= 656 B with a 16-B aligned stride");
   DSA_REQUIRE(out_stride >= 576 && out_stride % 8 == 0 && aligned16(out),
               "dsa_dequant_mla_paged: out must be 16-B aligned with out_stride %% 8 == 0 and >= 576");
-  hipLaunchKernelGGL(dequant_mla_kernel, dim3(grid_for(n_tokens * kMlaItems)), dim3(kDqThreads), 0,
-                     stream, cache, cache_stride_bytes, slots, n_tokens, out, out_stride);
+  const int64_t items = n_tokens * kMlaItems;
+  // up to 32768 CTAs (a thread's passes then stay few; measured 2% faster than 8192 at 393K tokens)
+  const dim3 grid(grid_for((items + kMlaUnroll - 1) / kMlaUnroll, 32768));
+  if (items + static_cast<int64_t>(grid.x) * kDqThreads * kMlaUnroll <= 0xFFFFFFFFll) {
+    hipLaunchKernelGGL(dequant_mla_kernel<uint32_t>, grid, dim3(kDqThreads), 0, stream, cache, cache_stride_bytes,
+                       slots, n_tokens, out, out_stride);
+  } else {
+    hipLaunchKernelGGL(dequant_mla_kernel<int64_t>, grid, dim3(kDqThreads), 0, stream, cache, cache_stride_bytes,
+                       slots, n_tokens, out, out_stride);
+  }
   return check_launch("dsa_dequant_mla_paged");
 }

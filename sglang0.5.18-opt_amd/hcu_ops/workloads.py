@@ -11,6 +11,10 @@ Workloads (indexer heads H x 128, page size 64, 132-B paged fp8 K cache with per
   prefill_8k_64k     8192 query rows over a 65536-token cached prefix (73728 keys, causal)
   prefill_16k_128k   16384 query rows over a 131072-token prefix (147456 keys, causal),
                      K drawn from Student-t(4) before quantisation
+  dequant_mla_393k   392832 tokens gathered at random from a 2^19-slot pool of 656-B MLA slots
+                     (the shape of prefill/microbench/mb_dequant.py:87-113); dequant_mla_131k the
+                     same with 131072 tokens
+  dequant_k_74k      the 73728 keys of prefill_8k_64k, gathered from its 132-B paged cache
 Draw order (decode): q ~ N(0,1) -> bf16; w ~ N(0, 1/8); page permutation; K ~ N(0,1) per pooled
 token (decode_mtp64 draws its request lengths from a second generator seeded seed + 1000).
 Prefill: q, w, page permutation, K.
@@ -179,6 +183,55 @@ def prefill_8k_64k():
 
 def prefill_16k_128k():
     return prefill_case(5, 16384, 131072, dist="student_t4", name="prefill_16k_128k")
+
+
+@dataclass
+class MlaDequantCase:
+    name: str
+    cache: torch.Tensor  # uint8 [pool, 1, 656]: [512 fp8 | 4 x f32 scale | 64 x bf16 rope]
+    slots: torch.Tensor  # int32 [n]
+
+    @property
+    def tokens(self):
+        return self.slots.shape[0]
+
+
+def mla_dequant_case(seed, n_tok, pool=1 << 19, name="dequant_mla"):
+    """A pool of MLA slots: fp8 codes drawn uniformly over the non-NaN codes, per-group scales in
+    [1e-3, 1.1e-2), bf16 rope ~ N(0,1); n_tok slots drawn uniformly from the pool (repeats
+    allowed, as the reference's microbenchmark draws them)."""
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 254, (pool, 512), generator=g, dtype=torch.int32)
+    codes = (codes + (codes >= 0x7F).int()).to(torch.uint8)  # skip 0x7F; 0xFF is never drawn
+    scale = torch.rand(pool, 4, generator=g) * 0.01 + 1e-3
+    rope = torch.randn(pool, 64, generator=g).to(torch.bfloat16)
+    cache = torch.cat([codes, scale.view(torch.uint8).view(pool, 16), rope.view(torch.uint8).view(pool, 128)], 1)
+    slots = torch.randint(0, pool, (n_tok,), generator=g, dtype=torch.int32)
+    return MlaDequantCase(name, cache.contiguous().view(pool, 1, 656), slots)
+
+
+@dataclass
+class KDequantCase:
+    name: str
+    kv: torch.Tensor     # uint8 [n_pages, 64, 1, 132]
+    slots: torch.Tensor  # int32 [n]
+
+    @property
+    def tokens(self):
+        return self.slots.shape[0]
+
+
+def dequant_mla_393k():
+    return mla_dequant_case(6, 392832, name="dequant_mla_393k")
+
+
+def dequant_mla_131k():
+    return mla_dequant_case(6, 131072, name="dequant_mla_131k")
+
+
+def dequant_k_74k():
+    c = prefill_8k_64k()
+    return KDequantCase("dequant_k_74k", c.kv, c.slots())
 
 
 # ---------------------------------------------------------------------------------------------

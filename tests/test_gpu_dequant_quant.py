@@ -49,17 +49,18 @@ def test_dequant_and_gather_random_cache(gpu):
     assert np.array_equal(sc.cpu().numpy().view(np.uint32), scale.view(np.uint32))
 
 
-def test_dequant_mla_656(gpu):
+@pytest.mark.parametrize("n", [1, 7, 3000, 250000])  # 250000: several grid-stride passes per thread
+def test_dequant_mla_656(gpu, n):
     g = torch.Generator().manual_seed(2)
     pool = 4096
     cache = (torch.randn(pool, 656, generator=g) * 0.1).to(torch.float8_e4m3fn).view(torch.uint8)
     cache[:, 512:528] = (torch.rand(pool, 4, generator=g) * 0.02 + 1e-3).view(torch.uint8)
     cache[:, 528:] = torch.randn(pool, 64, generator=g).to(torch.bfloat16).view(torch.uint8)
-    slots = torch.randint(0, pool, (3000,), generator=g, dtype=torch.int32)
+    slots = torch.randint(0, pool, (n,), generator=g, dtype=torch.int32)
     got = hcu_ops.dequantize_k_cache_paged(cache.view(torch.float8_e4m3fn).view(pool, 1, 656).to(gpu), slots.to(gpu))
-    assert tuple(got.shape) == (3000, 1, 576) and got.dtype == torch.bfloat16
+    assert tuple(got.shape) == (n, 1, 576) and got.dtype == torch.bfloat16
     ref = O.dequant_mla(cache.numpy(), slots.numpy())
-    assert np.array_equal(got.view(3000, 576).view(torch.int16).cpu().numpy().view(np.uint16), ref)
+    assert np.array_equal(got.view(n, 576).view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
 def test_quant_q_bit_exact(gpu):
