@@ -952,8 +952,9 @@ struct TopkArgs {
   int T;             // CTAs the balanced split kernel spreads the rows' tokens over
   int32_t* ghist;    // [rows][kBins]  pass-1 histogram
   int32_t* gcnt;     // [rows][2] = (positives, zeros)
-  int32_t* ctr;      // per row (stride ctr_stride): [0] output slots taken, [1] candidates
-                     // published, [2] slice CTAs finished -- zero before the split kernel
+  int32_t* ctr;      // per row (stride ctr_stride, 8-B aligned), zero before the split kernels:
+                     // exact split [0] output slots taken, [1] candidates published, [2] slice
+                     // CTAs finished; sampled split [0] candidates published, [1] CTAs finished
   int64_t ctr_stride;
   uint32_t* c_keys;  // [rows][kCapS] candidate keys published by the slice CTAs
   int32_t* c_tok;    // [rows][kCapS] their tokens
@@ -1220,7 +1221,7 @@ __device__ __forceinline__ bool split_slice(int len, int c, int j, int& begin, i
 // CTA of a row computes the same K* from the row's sample, collects its slice's keys >= K* and
 // publishes them (device-coherent stores at slots from the row's counter); the last CTA of the
 // row resolves them, or runs the exact path over the row when their count missed [2048, kCapS].
-// Counters (zero on entry): [1] keys published, [2] CTAs done.
+// Counters (zero on entry): words 0..1 as one 64-bit word (keys published, CTAs done).
 template <bool kVec>
 __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void topk_split_sampled_kernel(const TopkArgs a) {
   __shared__ SampledLds L;
@@ -1268,7 +1269,9 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
 
   const int n_loc = L.n[0];
   int32_t* ctr = a.ctr + static_cast<int64_t>(row) * a.ctr_stride;
-  if (tid == 0) L.n[1] = n_loc ? atomicAdd(&ctr[1], n_loc) : 0;
+  // words 0..1 of the row's counters as one 64-bit word: low = keys published, high = CTAs done
+  unsigned long long* const pub = reinterpret_cast<unsigned long long*>(ctr);
+  if (tid == 0) L.n[1] = n_loc ? static_cast<int>(atomicAdd(pub, static_cast<unsigned long long>(n_loc))) : 0;
   __syncthreads();
   uint32_t* lk = a.c_keys + static_cast<int64_t>(row) * kCapS;
   int32_t* lt = a.c_tok + static_cast<int64_t>(row) * kCapS;
@@ -1286,9 +1289,11 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const bool last = atomicAdd(&ctr[2], 1) == n_sl - 1;
+    // every CTA adds its count before its done mark, so the last mark returns the final count
+    const unsigned long long old = atomicAdd(pub, 1ull << 32);
+    const bool last = static_cast<int>(old >> 32) == n_sl - 1;
     L.n[2] = last;
-    L.n[3] = last ? __hip_atomic_load(&ctr[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    L.n[3] = last ? static_cast<int>(old & 0xFFFFFFFFull) : 0;
   }
   __syncthreads();
   if (!L.n[2]) return;
