@@ -250,7 +250,9 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
   }
 }
 
-template <int H, int R, bool kHist>
+// kMask = false: a.mask is null (prefill), known at compile time, so the page loop carries no
+// mask state.
+template <int H, int R, bool kHist, bool kMask>
 __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_waves_per_eu(
     Shape<R, kHist>::kWavesPerSimd))) void mqa_logits_decode_kernel(const DecodeArgs a) {
   constexpr int HT = H / 16;  // head tiles
@@ -361,7 +363,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     const int u0 = static_cast<int>(static_cast<int64_t>(units) * jc / nj);
     const int u1 = static_cast<int>(static_cast<int64_t>(units) * (jc + 1) / nj);
     const bool wide = (reinterpret_cast<uintptr_t>(a.mask) & 7u) == 0 && (a.mask_stride & 3) == 0;
-    for (int u = a.mask != nullptr ? u0 + tid : u1; u < u1; u += NT) {
+    for (int u = kMask && a.mask != nullptr ? u0 + tid : u1; u < u1; u += NT) {
       const int rr = u / tail;
       int16_t* m = a.mask + static_cast<int64_t>(row0 + rr) * a.mask_stride + (pages + u - rr * tail) * 4;
       if (wide) {
@@ -391,7 +393,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   auto flush = [&]() {
     if (pend_p < 0) return;
     const int token = pend_p * kPage + lane;
-    if (a.mask != nullptr && lane < 4)
+    if (kMask && a.mask != nullptr && lane < 4)
       *reinterpret_cast<int16_t*>(reinterpret_cast<char*>(mrow) + static_cast<uint32_t>((pend_p * 4 + lane) * 2)) =
           static_cast<int16_t>((pend_bits >> (16 * lane)) & 0xFFFFu);
     if (token < len) *reinterpret_cast<float*>(reinterpret_cast<char*>(lrow) + static_cast<uint32_t>(token * 4)) = pend_v;
@@ -450,7 +452,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     const float v = val * scale;
     pend_p = p;
     pend_v = v;
-    pend_bits = (a.mask != nullptr || kHist) ? __ballot(p * kPage + lane < len && __float_as_uint(v) != 0u) : 0;
+    pend_bits = ((kMask && a.mask != nullptr) || kHist) ? __ballot(p * kPage + lane < len && __float_as_uint(v) != 0u) : 0;
   };
   // the two slots of a stream are distinct LDS objects, so the compiler can tell that the
   // reads of one do not wait for the DMA into the other
@@ -526,8 +528,15 @@ __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __res
 
 template <int H, int R, bool kHist>
 void launch_one(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
-  hipLaunchKernelGGL((mqa_logits_decode_kernel<H, R, kHist>), dim3(grid), dim3(Shape<R, kHist>::kThreads), 0, stream,
-                     a);
+  if constexpr (R == 8) {  // eight rows a CTA: the prefill shape, which writes no mask
+    if (a.mask == nullptr) {
+      hipLaunchKernelGGL((mqa_logits_decode_kernel<H, R, kHist, false>), dim3(grid), dim3(Shape<R, kHist>::kThreads),
+                         0, stream, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((mqa_logits_decode_kernel<H, R, kHist, true>), dim3(grid), dim3(Shape<R, kHist>::kThreads), 0,
+                     stream, a);
 }
 
 template <int H, bool kHist>
