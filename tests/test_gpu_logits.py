@@ -174,3 +174,49 @@ def test_prefill_writes_only_below_len(gpu):
         assert not np.isnan(got[r, :L]).any(), f"row {r}: entries below len not written"
         assert np.isnan(got[r, L:]).all(), f"row {r}: entries at or past min(len, width) written"
         assert np.array_equal(got[r, :L], ref[r, :L]), f"row {r}: differs from the torch binding"
+
+
+def test_decode_wide_block_nontemporal_stores(gpu):
+    """A logits block above 16 MB (64 rows x 70,400-token capacity, 18 MB) takes the kernel's
+    nontemporal-store path: same bits as the same rows in a narrow block (cached stores), and the
+    oracle's values; entries past each row's length stay untouched."""
+    lens = [900 + 37 * i for i in range(32)]
+    wide = wl.decode_case(41, lens, group=2, heads=64, bt_pages=1100)
+    narrow = wl.decode_case(41, lens, group=2, heads=64)
+    assert wide.rows * wide.width * 4 > (16 << 20) and narrow.rows * narrow.width * 4 < (16 << 20)
+    _, _, lg_w, mask_w = _run_decode(wide, gpu, rpc=2)
+    _, _, lg_n, mask_n = _run_decode(narrow, gpu, rpc=2)
+    keep = torch.arange(narrow.width, device=gpu)[None, :] < narrow.context_lens.to(gpu)[:, None]
+    assert torch.equal(lg_w[:, :narrow.width][keep].view(torch.int32), lg_n[keep].view(torch.int32))
+    assert torch.equal(mask_w[:, :narrow.width // 16], mask_n)
+    assert not mask_w[:, narrow.width // 16 + 1:].any()
+    _check_decode(wide, lg_w, mask_w)
+
+
+def test_prefill_wide_block_nontemporal_stores(gpu):
+    """Prefill into a 64-row x 70,016-wide block (17.9 MB, nontemporal stores) with short causal
+    rows: the oracle's values below each row's length, nothing written past it."""
+    case = wl.prefill_case(43, 64, 1000, heads=64)
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    width = 70016
+    assert case.rows * width * 4 > (16 << 20)
+    bt = torch.cat([case.block_table, torch.zeros(width // 64 - case.block_table.numel(), dtype=torch.int32)])
+    out = torch.full((case.rows, width), float("nan"), device=gpu)
+    import ctypes
+    import os
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(hcu_ops.__file__), "libdsa_indexer.so"))
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    f = lib.dsa_mqa_logits_prefill
+    f.argtypes = [P, P, I, I64, P, I64, P, I64, P, P, I64, I64, P]
+    lib.dsa_last_error.restype = ctypes.c_char_p
+    kv, btd, lens = case.kv.to(gpu), bt.to(gpu), case.lens.to(gpu)
+    st = f(q8.data_ptr(), w.data_ptr(), 64, case.rows, kv.data_ptr(), kv.stride(0), btd.data_ptr(), btd.numel(),
+           lens.data_ptr(), out.data_ptr(), out.stride(0), width, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.dsa_last_error()
+    rq8, rw = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
+    ref, mag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), bt.numpy(), case.lens.numpy(), case.n_keys)
+    got = out.cpu().numpy()
+    for r in range(case.rows):
+        L = int(case.lens[r])
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
+        assert np.isnan(got[r, L:]).all(), f"row {r}: entries past len written"
