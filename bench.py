@@ -1,9 +1,10 @@
 """Benchmark of the MI355X DSA indexer path (one GPU).
 
 A step is one pass of the indexer over one batch with every input resident in HBM:
-  decode   bf16 q -> fp8 quant -> paged fp8 MQA logits (+ fused top-k pass 1) -> top-2048 +
+  decode   bf16 q -> fp8 quant -> paged fp8 MQA logits (+ the paired top-k's workspace) -> top-2048 +
            page-table remap
-  prefill  paged K dequant to bf16 -> q quant -> causal fp8 MQA logits -> top-2048 + remap
+  prefill  bf16 q -> fp8 quant -> causal fp8 MQA logits over the paged K in 4096-row slabs, each
+           slab's top-2048 + remap behind it (hcu_ops.prefill_indexer)
 Steps are captured in a hipGraph (--steps-per-graph of them per graph, as a serving loop
 captures the indexer inside its model step) and replayed.  The step graph first runs untimed
 for --settle-ms (the GPU raises its clocks only after some milliseconds of load; a serving loop
@@ -32,6 +33,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "sglang0.5.18-opt_amd"))
 sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))  # the seeded workload generators
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA
@@ -107,13 +109,12 @@ class DecodeStep:
 
     def logits_only(self, hist=False):
         """The dominant kernel alone (the step's launch shape, q already quantised); hist=True also
-        prepares the paired top-k's workspace (its counters zeroed), as inside the step."""
+        prepares the paired top-k's workspace as inside the step."""
         if not hasattr(self, "_q8"):
             self._q8, self._w8 = self.h.quant_q_fp8(self.q, self.w)
         c = self.case
-        return self.h._C.mqa_logits_hist(self._q8.unsqueeze(1), self.kv, self._w8, self.lens, self.bt, c.width,
-                                         c.group, 0, 1 if c.group == 1 else self.h._MQA_RPC,
-                                         self.lens if hist else None, hist and self.h._MQA_FUSED_PASS1)
+        return self.h.mqa_logits(self._q8.unsqueeze(1), self.kv, self._w8, self.lens, self.bt, c.width, c.group,
+                                 hist_lens=self.lens if hist else None)
 
     def tokens(self):
         return self.case.tokens_scored()
@@ -183,24 +184,19 @@ class PrefillStep:
         g = lambda t: t.to(dev)
         self.q, self.w, self.kv, self.bt, self.lens = g(case.q), g(case.w), g(case.kv), g(case.block_table), \
             g(case.lens)
-        self.slots = g(case.slots())
-        self.pt = self.slots.view(1, -1)
+        self.pt = g(case.slots())
         self.width = case.n_keys
         self.out = torch.empty(case.rows, 2048, dtype=torch.int32, device=dev)
         self.slab = min(self.SLAB, case.rows)
-        tail = case.rows % self.slab
-        self.cu = torch.tensor([0, self.slab], dtype=torch.int32, device=dev)
-        self.cu_tail = torch.tensor([0, tail if tail else self.slab], dtype=torch.int32, device=dev)
 
     def __call__(self):
+        # the logits kernel reads the paged fp8 K directly, so no dequantised copy of K is made;
+        # logits in 4096-row slabs (the budget of 4096 rows of f32 logits), each slab's top-2048
+        # right behind it
         h = self.h
-        self.kbf16 = h.dequant_k_paged(self.kv, self.slots)
         q8, w = h.quant_q_fp8(self.q, self.w)
-        for r0 in range(0, self.case.rows, self.slab):
-            r1 = min(r0 + self.slab, self.case.rows)
-            lg = h.mqa_logits_prefill(q8[r0:r1], w[r0:r1], self.kv, self.bt, self.lens[r0:r1], self.width)
-            cu = self.cu if r1 - r0 == self.slab else self.cu_tail
-            h.topk_transform(lg, self.lens[r0:r1], self.pt, cu, out=self.out[r0:r1])
+        h.prefill_indexer(q8, w, self.kv, self.bt, self.lens, self.width, self.pt,
+                          memory_budget_bytes=self.slab * self.width * 4, max_slab_rows=self.slab, out=self.out)
         return self.out
 
     def logits_only(self):
@@ -373,7 +369,7 @@ def main(argv=None):
         return 2
 
     import torch
-    from hcu_ops import workloads as wl
+    import workloads as wl
 
     dev = torch.device("cuda:0")
     if args.copy_calibration_mib > 0:
@@ -464,7 +460,7 @@ def main(argv=None):
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "K-tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)", "data": "synthetic (seeded, see workloads.py)",
+        "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)", "data": "synthetic (seeded, see tests/workloads.py)",
         "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "query_rows": int(case.rows),
                    "tokens_scored_per_step": int(tokens),
                    "graph": f"hipGraph of {per} steps per replay",
@@ -494,7 +490,7 @@ def dequant_report(args, case, step, ms, per, torch):
     line = {
         "metric": DEQUANT_METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp8e4m3 -> bf16", "data": "synthetic (seeded, see workloads.py)",
+        "vs_baseline": None, "dtype": "fp8e4m3 -> bf16", "data": "synthetic (seeded, see tests/workloads.py)",
         "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "tokens": int(case.tokens),
                    "bytes_per_token": step.tok_bytes, "graph": f"hipGraph of {per} launches per replay",
                    "settle_ms": args.settle_ms},

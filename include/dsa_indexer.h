@@ -102,11 +102,13 @@ int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* s
  * request (<= 0: as many as are resident at once); the grid is target_ctas + B / rows_per_cta.
  * hist_ws (nullable, int32 [B * (2 * 4096 + 2)], 16-B aligned): the pass-1 workspace of a
  * following dsa_topk_transform_pre, in its layout [12-bit histograms rows*4096 | second block
- * rows*4096 | (positives, zeros) rows*2]; of the second block only words 0..2 of each row are
- * used (the split top-k's per-row counters).  fuse_pass1 = 0: only those counters are zeroed
- * (the top-k then selects with its sampled threshold, no pass 1); fuse_pass1 = 1 (needs hist_lens, int32 [B], and rows_per_cta <= 3): pass 1
+ * rows*4096 | (positives, zeros) rows*2]; of the second block the top-k uses words 0..2 of each
+ * row (its per-row counters).  fuse_pass1 = 1 (needs hist_lens, int32 [B], and
+ * rows_per_cta <= 3; the reference's fused kHist path, mqa_hist.cu:135-138,219-304): pass 1
  * (12-bit key histogram + positive / zero counts of every row whose min(hist_lens[r], width) >
- * 2048) is built here, inside the logits kernel (reference: the fused kHist path). */
+ * 2048) is built here, inside the logits kernel, and the second block is zeroed whole.
+ * fuse_pass1 = 0: only the counters are zeroed, inside the logits kernel (no extra launch); the
+ * top-k then selects with its sampled threshold. */
 int dsa_mqa_logits_decode(const uint8_t* q8, const float* w, int heads, int64_t batch,
                           int group_size, const uint8_t* kv_cache, int64_t page_stride_bytes,
                           const int32_t* context_lens, const int32_t* block_table,
@@ -146,10 +148,14 @@ int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int heads, int64_t
  * Only the selected set is the contract; the order within a row is unspecified.
  * score f32 [rows, width] row stride score_stride; mask i16 [rows, ceil(width/16)] row stride
  * mask_stride; lengths i32 [rows]; page_table i32 with pt_cols entries per row (tokens at or past
- * pt_cols map to -1) and row stride pt_stride; out i32 [rows, 2048].
+ * pt_cols map to -1) and row stride pt_stride (0: every row reads the same page-table row, e.g.
+ * the query rows of one prefill request); out i32 [rows, 2048].
  * max_splits: CTAs a row may be split over (1 = one CTA per row).
  */
 size_t dsa_topk_workspace_bytes(int64_t rows, int64_t width, int max_splits, int n_cu);
+/* CTAs per row the top-k splits [rows, width] scores over (1: one CTA per row); the role of the
+ * reference's _topk_splits (hcu_ops/hcu_ops/__init__.py:61-66) with this build's split policy. */
+int dsa_topk_split_count(int64_t rows, int64_t width, int max_splits, int n_cu);
 int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
                        const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
                        int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
@@ -169,6 +175,29 @@ int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t wid
                            const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
                            int32_t* hist_ws, int pass1_done, void* workspace, size_t workspace_bytes,
                            int32_t* out, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Prefill indexer of one request (the role of sglang's prefill indexer under
+ * SGLANG_NSA_MQA_LOGITS_MEMORY_BUDGET_GB, prefill/p_opt.sh:58, at the cached-prefix call site
+ * prefill/README.md:56-61; its kernels, lightop _mqa_logits + adaptive_topk, are not vendored):
+ * the query rows are scored in slabs of slab_rows rows -- dsa_mqa_logits_prefill into the
+ * workspace's logits slab [slab_rows, width] f32, then dsa_topk_transform of the slab's rows,
+ * every row reading the request's one page-table row `page_table` (pt_cols entries, token ->
+ * slot) -- so no more than one slab of logits ever exists.
+ *   out[r, :] = the top-2048 (ties to the lower token) of row r's logits over keys t < lens[r],
+ *               as page_table[t], -1 padded when min(lens[r], width) < 2048.
+ * q8 / w / kv_cache / block_table / lens as in dsa_mqa_logits_prefill; out int32 [rows, 2048].
+ * dsa_prefill_slab_rows gives the slab size a byte budget of logits allows (a multiple of 8
+ * rows when at least 8 fit, capped at max_slab_rows > 0 and at rows);
+ * dsa_prefill_indexer_workspace_bytes the workspace (256-B aligned) the call needs. */
+int64_t dsa_prefill_slab_rows(int64_t rows, int64_t width, int64_t max_slab_rows, int64_t memory_budget_bytes);
+size_t dsa_prefill_indexer_workspace_bytes(int64_t rows, int64_t width, int64_t slab_rows, int max_splits,
+                                           int n_cu);
+int dsa_prefill_indexer(const uint8_t* q8, const float* w, int heads, int64_t rows, const uint8_t* kv_cache,
+                        int64_t page_stride_bytes, const int32_t* block_table, int64_t bt_pages,
+                        const int32_t* lens, int64_t width, const int32_t* page_table, int64_t pt_cols,
+                        int64_t slab_rows, int max_splits, int n_cu, void* workspace, size_t workspace_bytes,
+                        int32_t* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -130,16 +130,21 @@ def mqa_logits_decode(q8, w, kv, context_lens, block_table, group, width):
     logits = np.full((B, width), np.nan)
     mag = np.zeros((B, width))
     bits = np.zeros((B, width), dtype=bool)
-    for r in range(B):
-        L = int(np.clip(context_lens[r], 0, width))
-        if L == 0:
+    lens = np.clip(np.asarray(context_lens, dtype=np.int64), 0, width)
+    for g0 in range(0, B, group):
+        n = int(lens[g0:g0 + group].max()) if B else 0
+        if n == 0:
             continue
-        g0 = (r // group) * group
-        codes, scale = kv_tokens(kv, slots_of(block_table[g0], L))
-        lg, mg = logits_row(q8[r], w[r], codes, scale)
-        logits[r, :L] = lg
-        mag[r, :L] = mg
-        bits[r, :L] = lg != 0.0
+        # the group's keys are gathered once; every row of the group reads a prefix of them
+        codes, scale = kv_tokens(kv, slots_of(block_table[g0], n))
+        for r in range(g0, g0 + group):
+            L = int(lens[r])
+            if L == 0:
+                continue
+            lg, mg = logits_row(q8[r], w[r], codes[:L], scale[:L])
+            logits[r, :L] = lg
+            mag[r, :L] = mg
+            bits[r, :L] = lg != 0.0
     return logits, mag, pack_mask(bits)
 
 

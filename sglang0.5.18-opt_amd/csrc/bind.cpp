@@ -40,10 +40,15 @@ void check_kv(const torch::Tensor& kv_cache) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Logits (hcu_ops/csrc/mqa_hist.cu:324-405).  persistent_ctas > 0 sets the number of CTAs the
-// K pages are spread over (<= 0: every CTA resident at once).  hist_lens: also return zws, the
-// top-k's workspace, its per-row counters zeroed (the paired top-k selects with its sampled
-// threshold) or, with fuse_pass1, with pass 1 built inside the logits kernel.
+// Logits (hcu_ops/csrc/mqa_hist.cu:324-405).  persistent_ctas keeps the reference's meaning, CTAs
+// per request row-set (its grid is persistent_ctas * B / rows_per_cta CTAs): > 0 spreads the K
+// pages over that many CTAs in total, the balanced grid giving each row-set a share by its page
+// count; <= 0 (the reference's lightop default and its -1 policy) takes every CTA that is
+// resident at once.  hist_lens: also return zws, the paired split top-k's workspace.  With
+// fuse_pass1 (the default, the reference's contract) pass 1 is built inside the logits kernel:
+// zws = [12-bit key histograms | zeros | (positives, zeros)] of the rows longer than 2048
+// (mqa_hist.cu:278-304); fuse_pass1 = false zeroes only the split top-k's per-row counters in
+// zws (the paired top-k then selects with its sampled threshold: no histogram is built).
 std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::Tensor& kv_cache,
                                            const torch::Tensor& weights, const torch::Tensor& context_lens,
                                            const torch::Tensor& block_table, int64_t max_context_len,
@@ -79,12 +84,16 @@ std::vector<torch::Tensor> mqa_logits_hist(const torch::Tensor& q, const torch::
   auto mask = torch::empty({B, mask_stride}, q.options().dtype(at::kShort));
   auto zws = torch::empty({hist ? B * (2 * kBins + 2) : 0}, q.options().dtype(at::kInt));
   const int64_t pages = block_table.size(1);
-  const int target = static_cast<int>(std::min<int64_t>(std::max<int64_t>(persistent_ctas, 0), 1 << 20));
+  const int64_t R = rows_per_cta > 0 ? rows_per_cta : (group_size % 2 == 0 ? 2 : 1);
+  TORCH_CHECK(!(hist && fuse_pass1) || R <= 3,
+              "the fused pass-1 histogram needs rows_per_cta <= 3 (pass fuse_pass1=False for more)");
+  const int64_t per_set = std::min<int64_t>(std::max<int64_t>(persistent_ctas, 0), 1 << 16);
+  const int target = static_cast<int>(std::min<int64_t>(per_set * (B / std::max<int64_t>(R, 1)), 1 << 24));
   check_status(dsa_mqa_logits_decode(
       reinterpret_cast<const uint8_t*>(q.data_ptr()), weights.data_ptr<float>(), static_cast<int>(H), B,
       static_cast<int>(group_size), kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0), context_lens.data_ptr<int>(),
       block_table.data_ptr<int>(), block_table.stride(0), pages, logits.data_ptr<float>(), logits.stride(0),
-      mask.data_ptr<int16_t>(), mask_stride, static_cast<int>(rows_per_cta), target,
+      mask.data_ptr<int16_t>(), mask_stride, static_cast<int>(R), target,
       hist ? hist_lens->data_ptr<int>() : nullptr, hist ? zws.data_ptr<int>() : nullptr, hist && fuse_pass1 ? 1 : 0,
       cur_stream()));
   return {logits, mask, zws};
@@ -299,15 +308,71 @@ torch::Tensor mqa_logits_prefill(const torch::Tensor& q, const torch::Tensor& we
   return logits;
 }
 
+// Prefill indexer of one request (dsa_prefill_indexer): logits in slabs of at most
+// max_slab_rows rows and memory_budget_bytes of f32 logits, each slab's top-2048 behind it.
+// page_table_1: int32 [>= width] token -> slot of the request (the remap of the output).
+torch::Tensor prefill_indexer(const torch::Tensor& q, const torch::Tensor& weights, const torch::Tensor& kv_cache,
+                              const torch::Tensor& block_table, const torch::Tensor& lens, int64_t width,
+                              const torch::Tensor& page_table_1, int64_t memory_budget_bytes, int64_t max_slab_rows,
+                              int64_t max_splits, const c10::optional<torch::Tensor>& out) {
+  TORCH_CHECK(q.is_cuda() && q.scalar_type() == at::kFloat8_e4m3fn && q.dim() == 3 &&
+                  (q.size(1) == 32 || q.size(1) == 64) && q.size(2) == kHeadDim && q.is_contiguous(),
+              "q must be contiguous fp8 e4m3fn [rows, H, 128] with H in {32, 64}");
+  const int64_t rows = q.size(0);
+  const int64_t H = q.size(1);
+  check_kv(kv_cache);
+  TORCH_CHECK(weights.scalar_type() == at::kFloat && weights.dim() == 2 && weights.size(0) == rows &&
+                  weights.size(1) == H && weights.is_contiguous(),
+              "weights must be contiguous float32 [rows, H]");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && block_table.dim() == 1 && block_table.is_contiguous(),
+              "block_table must be contiguous int32 [pages]");
+  TORCH_CHECK(lens.scalar_type() == at::kInt && lens.dim() == 1 && lens.size(0) == rows && lens.is_contiguous(),
+              "lens must be contiguous int32 [rows]");
+  TORCH_CHECK(page_table_1.scalar_type() == at::kInt && page_table_1.dim() == 1 && page_table_1.is_contiguous(),
+              "page_table_1 must be contiguous int32 [tokens]");
+  TORCH_CHECK(width > 0 && width <= block_table.size(0) * kPage, "width must be within the block table capacity");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  torch::Tensor dst;
+  if (out.has_value()) {
+    TORCH_CHECK(out->is_cuda() && out->scalar_type() == at::kInt && out->dim() == 2 && out->size(0) == rows &&
+                    out->size(1) == kTopK && out->is_contiguous(),
+                "out must be a contiguous int32 [rows, 2048] tensor");
+    dst = *out;
+  } else {
+    dst = torch::empty({rows, kTopK}, q.options().dtype(at::kInt));
+  }
+  if (rows == 0) return dst;
+  const int cus = n_cu();
+  const int splits = static_cast<int>(std::max<int64_t>(1, max_splits));
+  const int64_t slab = dsa_prefill_slab_rows(rows, width, max_slab_rows, memory_budget_bytes);
+  const size_t ws_bytes = dsa_prefill_indexer_workspace_bytes(rows, width, slab, splits, cus);
+  auto ws = torch::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  check_status(dsa_prefill_indexer(reinterpret_cast<const uint8_t*>(q.data_ptr()), weights.data_ptr<float>(),
+                                   static_cast<int>(H), rows, kv_cache.data_ptr<uint8_t>(), kv_cache.stride(0),
+                                   block_table.data_ptr<int>(), block_table.size(0), lens.data_ptr<int>(), width,
+                                   page_table_1.data_ptr<int>(), page_table_1.size(0), slab, splits, cus,
+                                   ws.data_ptr(), ws_bytes, dst.data_ptr<int>(), cur_stream()));
+  return dst;
+}
+
+int64_t topk_splits(int64_t rows, int64_t width, int64_t max_splits, int64_t cus) {
+  return dsa_topk_split_count(rows, width, static_cast<int>(std::max<int64_t>(1, max_splits)),
+                              static_cast<int>(cus > 0 ? cus : n_cu()));
+}
+
+int64_t prefill_slab_rows(int64_t rows, int64_t width, int64_t memory_budget_bytes, int64_t max_slab_rows) {
+  return dsa_prefill_slab_rows(rows, width, max_slab_rows, memory_budget_bytes);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mqa_logits_hist", &mqa_logits_hist,
         "paged fp8 MQA indexer logits + 16-token nonzero mask -> {logits, mask, zws}; with hist_lens zws is the "
-        "paired top-k's workspace (counters zeroed, or pass 1 filled when fuse_pass1)",
+        "paired split top-k's workspace with pass 1 built (fuse_pass1, the default) or only its counters zeroed",
         py::arg("q"), py::arg("kv_cache"), py::arg("weights"), py::arg("context_lens"), py::arg("block_table"),
         py::arg("max_context_len"), py::arg("group_size"), py::arg("persistent_ctas"), py::arg("rows_per_cta"),
-        py::arg("hist_lens"), py::arg("fuse_pass1") = false);
+        py::arg("hist_lens"), py::arg("fuse_pass1") = true);
   m.def("sparse_mask_topk_transform", &sparse_mask_topk_transform,
         "Exact top-2048 + page-table transform over sparse-mask MQA logits (one CTA per row)");
   m.def("sparse_mask_topk_transform_split", &sparse_mask_topk_transform_split,
@@ -316,7 +381,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "sparse_mask_topk_transform_split on mqa_logits_hist's pass-1 workspace (pass1_done: built there)",
         py::arg("score"), py::arg("nonzero_mask"), py::arg("lengths"), py::arg("page_table_size_1"),
         py::arg("cu_seqlens_q"), py::arg("topk"), py::arg("max_splits"), py::arg("zws"),
-        py::arg("pass1_done") = false);
+        py::arg("pass1_done") = true);
   m.def("topk_transform", &topk_transform, "Exact top-2048 + page-table transform over dense scores (into out if given)",
         py::arg("score"), py::arg("lengths"), py::arg("page_table_size_1"), py::arg("cu_seqlens_q"), py::arg("topk"),
         py::arg("max_splits"), py::arg("out") = py::none());
@@ -326,4 +391,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("quant_q_fp8", &quant_q_fp8, "per-(row, head) fp8 quant of bf16 q -> (q8, weights * scale)");
   m.def("store_k_cache", &store_k_cache, "per-token fp8 quant of bf16 k into the 132-B paged K cache");
   m.def("mqa_logits_prefill", &mqa_logits_prefill, "prefill fp8 MQA indexer logits over one request's paged K");
+  m.def("prefill_indexer", &prefill_indexer,
+        "prefill indexer of one request: logits in budget-bounded row slabs, each slab's top-2048 + page-table "
+        "transform behind it -> int32 [rows, 2048]",
+        py::arg("q"), py::arg("weights"), py::arg("kv_cache"), py::arg("block_table"), py::arg("lens"),
+        py::arg("width"), py::arg("page_table_1"), py::arg("memory_budget_bytes"), py::arg("max_slab_rows"),
+        py::arg("max_splits"), py::arg("out") = py::none());
+  m.def("topk_splits", &topk_splits, "CTAs per row the split top-k uses for [rows, width] scores (1: one per row)",
+        py::arg("rows"), py::arg("width"), py::arg("max_splits"), py::arg("n_cu") = 0);
+  m.def("prefill_slab_rows", &prefill_slab_rows, "rows per logits slab of prefill_indexer for a byte budget");
 }

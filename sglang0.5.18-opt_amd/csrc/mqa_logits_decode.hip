@@ -512,11 +512,11 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   }
 }
 
-// Seeds the top-k pass-1 workspace: every token below min(hist_len, width) counts as a zero
-// until the logits kernel subtracts its nonzero ones.  Rows with <= 2048 tokens stay empty.
-// Of the second histogram block of the layout ([ghist1 | ghist2 | cnt], the reference's
-// workspace size) only words 0..2 of each row are used -- as the split top-k's per-row counters
-// -- and zeroed.
+// Seeds the top-k pass-1 workspace (mqa_hist.cu:278-304): every token below
+// min(hist_len, width) counts as a zero until the logits kernel subtracts its nonzero ones; rows
+// with <= 2048 tokens stay empty.  The second histogram block of the layout ([ghist1 | ghist2 |
+// cnt], the reference's workspace) is zeroed whole, as the reference leaves it; of it the split
+// top-k uses words 0..2 of each row as its per-row counters.
 __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __restrict__ hist_lens, int width,
                                                             int64_t batch, int32_t* __restrict__ ws) {
   const int64_t row = blockIdx.x;
@@ -524,13 +524,16 @@ __global__ __launch_bounds__(256) void mqa_hist_init_kernel(const int32_t* __res
   h = h < width ? h : width;
   const int zeros = h > kTopK ? h : 0;
   int4* g1 = reinterpret_cast<int4*>(ws + row * kBins);
-  for (int i = threadIdx.x; i < kBins / 4; i += 256) g1[i] = make_int4(i == kZeroBin / 4 ? zeros : 0, 0, 0, 0);
+  int4* g2 = reinterpret_cast<int4*>(ws + (batch + row) * kBins);
+  for (int i = threadIdx.x; i < kBins / 4; i += 256) {
+    g1[i] = make_int4(i == kZeroBin / 4 ? zeros : 0, 0, 0, 0);
+    g2[i] = make_int4(0, 0, 0, 0);
+  }
   if (threadIdx.x == 0) {
     int32_t* c = ws + 2 * batch * kBins + 2 * row;
     c[0] = 0;
     c[1] = zeros;
   }
-  if (threadIdx.x < 3) ws[(batch + row) * kBins + threadIdx.x] = 0;
 }
 
 template <int H, int R, bool kHist>

@@ -1484,7 +1484,8 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
   DSA_REQUIRE(mask == nullptr || mask_stride >= (width + 15) / 16, "%s: mask_stride < ceil(width / 16)", who);
   DSA_REQUIRE(cu_seqlens_q == nullptr || n_req >= 1, "%s: cu_seqlens_q needs n_req >= 1", who);
   DSA_REQUIRE(max_splits >= 1, "%s: max_splits must be >= 1", who);
-  DSA_REQUIRE(pt_cols >= 0 && pt_stride >= pt_cols, "%s: page-table row stride < its entries per row", who);
+  DSA_REQUIRE(pt_cols >= 0 && (pt_stride >= pt_cols || pt_stride == 0),
+              "%s: page-table row stride < its entries per row (and not 0)", who);
   const bool vec = width % 4 == 0 && score_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(score) & 15u) == 0;
 
   TopkArgs a;
@@ -1563,6 +1564,10 @@ int topk_common(const float* score, int64_t score_stride, int64_t width, const i
 }  // namespace dsa
 
 using namespace dsa;
+
+extern "C" int dsa_topk_split_count(int64_t rows, int64_t width, int max_splits, int n_cu) {
+  return split_count(rows, width, max_splits < 1 ? 1 : max_splits, n_cu);
+}
 
 extern "C" size_t dsa_topk_workspace_bytes(int64_t rows, int64_t width, int max_splits, int n_cu) {
   const int S = split_count(rows, width, max_splits < 1 ? 1 : max_splits, n_cu);

@@ -17,24 +17,37 @@ import torch  # noqa: F401  (loads libtorch / the HIP runtime before the extensi
 
 from . import _C
 
-# split: few rows are spread over up to HCU_TOPK_SPLITS CTAs each (default; one CTA per row
-#        once rows >= CUs / 2); single: always one CTA per row.
+# HCU_TOPK_IMPL: "split" (default) lets the top-k spread a row over up to HCU_TOPK_SPLITS CTAs while
+# the rows are few; "single" keeps one CTA per row.
 _TOPK_IMPL = os.environ.get("HCU_TOPK_IMPL", "split")
 _TOPK_SPLITS = int(os.environ.get("HCU_TOPK_SPLITS", "8"))
 
-# HCU_MQA_PCTAS[_G1]: CTAs the K pages of grouped [single] rows are spread over (each CTA streams a
-# slice of one request); <= 0 uses twice the CU count.  HCU_MQA_RPC: rows sharing one K stream
-# for groups (must divide the group).
-# HCU_MQA_HIST_MAX_ROWS: up to this many rows, mqa_logits(..., hist_lens) hands the paired top-k a
-# workspace whose counters it zeroed (saving the top-k's zeroing launch; the top-k then selects
-# with its sampled threshold); HCU_MQA_FUSED_PASS1=1 builds the exact pass 1 inside the logits
-# kernel instead (slower on gfx950: its LDS histogram lowers the logits kernel's occupancy).
+# Logits launch and its pairing with the top-k (the reference's knob names and meanings):
+#   HCU_MQA_PCTAS[_G1]   CTAs per request row-set for grouped [single] rows; <= 0 takes every CTA that
+#                        is resident at once (on gfx950 that beats the reference's -1 policy of 64 per
+#                        row-set for few rows: the balanced grid spreads the pages over the whole chip).
+#   HCU_MQA_RPC          rows of a group sharing one K page stream (must divide the group).
+#   HCU_MQA_HIST_MAX_ROWS[_G6]  up to this many single [grouped] rows, when the paired top-k will split
+#                        rows, mqa_logits(..., hist_lens) builds the top-k's pass-1 histogram inside the
+#                        logits kernel (rows_per_cta <= 3).
+#   HCU_MQA_PAIR_MAX_ROWS (this build's addition) otherwise, up to this many rows, the logits kernel
+#                        only zeroes the paired split top-k's per-row counters on its way, which saves
+#                        the top-k its zeroing launch; the top-k then selects against its sampled
+#                        threshold.  Measured on gfx950 for the 64-request MTP decode (G = 2): the
+#                        fused histogram's 8 KB of LDS counters per row cost the logits kernel more
+#                        occupancy than the histogram saves the top-k, hence 0 for grouped rows.
 _MQA_PCTAS = int(os.environ.get("HCU_MQA_PCTAS", "0"))
 _MQA_PCTAS_G1 = int(os.environ.get("HCU_MQA_PCTAS_G1", str(_MQA_PCTAS)))
 _MQA_RPC = int(os.environ.get("HCU_MQA_RPC", "2"))
-_MQA_HIST_MAX_ROWS = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS", "256"))
-_MQA_FUSED_PASS1 = os.environ.get("HCU_MQA_FUSED_PASS1", "0") == "1"
+_MQA_HIST_MAX_ROWS = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS", "8"))
+_MQA_HIST_MAX_ROWS_G6 = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS_G6", "0"))
+_MQA_PAIR_MAX_ROWS = int(os.environ.get("HCU_MQA_PAIR_MAX_ROWS", "256"))
 _MQA_HIST = None  # (logits, hist_lens, zws, pass1_done) of the last mqa_logits with hist_lens
+_N_CU = None
+# Prefill: SGLANG_NSA_MQA_LOGITS_MEMORY_BUDGET_GB bounds the logits slab of prefill_indexer, as it
+# bounds sglang's prefill indexer (reference prefill/p_opt.sh:58); slabs hold at most 4096 rows.
+_PREFILL_BUDGET = int(float(os.environ.get("SGLANG_NSA_MQA_LOGITS_MEMORY_BUDGET_GB", "2")) * (1 << 30))
+_PREFILL_MAX_SLAB_ROWS = 4096
 _HEADS = (32, 64)
 
 
@@ -78,23 +91,35 @@ def mqa_logits_supported(q, kv_cache, weights, group_size, context_lens=None, bl
     return ok
 
 
+def _topk_splits(rows, width):
+    """CTAs per row the paired split top-k will use for [rows, width] scores (reference
+    hcu_ops/hcu_ops/__init__.py:61-66, with this build's split policy)."""
+    global _N_CU
+    if _N_CU is None:
+        _N_CU = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    return _C.topk_splits(rows, width, _TOPK_SPLITS, _N_CU)
+
+
 def mqa_logits(q, kv_cache, weights, context_lens, block_table, max_context_len, group_size, hist_lens=None,
                persistent_ctas=None, rows_per_cta=None):
     """(logits f32 [B, max_context_len], mask i16 [B, max_context_len/16]) of the paged indexer
     (reference hcu_ops/hcu_ops/__init__.py:82-105).
 
     hist_lens: lengths of the paired sparse_mask_topk_transform; when that call will split rows,
-    its workspace is prepared here (counters zeroed, or pass 1 filled when HCU_MQA_FUSED_PASS1=1)."""
+    its workspace is prepared here (pass 1 built, or its counters zeroed; see the knobs above)."""
     global _MQA_HIST
     rows = q.shape[0]
     if persistent_ctas is None:
         persistent_ctas = _MQA_PCTAS_G1 if group_size == 1 else _MQA_PCTAS
     if rows_per_cta is None:
         rows_per_cta = 1 if group_size == 1 else _MQA_RPC
-    use_hist = (hist_lens is not None and _TOPK_IMPL == "split" and rows <= _MQA_HIST_MAX_ROWS
+    hist_max_rows = _MQA_HIST_MAX_ROWS if group_size == 1 else _MQA_HIST_MAX_ROWS_G6
+    use_hist = (hist_lens is not None and _TOPK_IMPL == "split"
+                and rows <= max(hist_max_rows, _MQA_PAIR_MAX_ROWS)
                 and hist_lens.dtype == torch.int32 and hist_lens.dim() == 1
-                and hist_lens.shape[0] == rows and hist_lens.is_contiguous())
-    fused = use_hist and _MQA_FUSED_PASS1 and rows_per_cta <= 3
+                and hist_lens.shape[0] == rows and hist_lens.is_contiguous()
+                and _topk_splits(rows, max_context_len) > 1)
+    fused = use_hist and rows <= hist_max_rows and rows_per_cta <= 3
     logits, mask, zws = _C.mqa_logits_hist(q, kv_cache, weights, context_lens.view(-1), block_table,
                                            max_context_len, group_size, persistent_ctas, rows_per_cta,
                                            hist_lens if use_hist else None, fused)
@@ -140,3 +165,23 @@ def topk_transform(score, lengths, page_table_size_1, cu_seqlens_q, topk=2048, m
     if max_splits is None:
         max_splits = _TOPK_SPLITS if _TOPK_IMPL == "split" else 1
     return _C.topk_transform(score, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, out)
+
+
+def prefill_indexer(q, weights, kv_cache, block_table, lens, width, page_table_1=None, memory_budget_bytes=None,
+                    max_slab_rows=None, out=None):
+    """Top-2048 slots of every query row of one prefill request: int32 [rows, 2048].
+
+    q fp8 [rows, H, 128] and weights f32 [rows, H] (quant_q_fp8's outputs), the request's paged
+    K (block_table int32 [pages]), lens int32 [rows] (causal: prefix + i + 1), width = keys of the
+    request.  The logits are scored in row slabs of at most memory_budget_bytes (default
+    SGLANG_NSA_MQA_LOGITS_MEMORY_BUDGET_GB) and max_slab_rows (default 4096) rows, each slab's
+    top-2048 selected right behind it, so at most one slab of logits exists.  page_table_1:
+    int32 [>= width] token -> slot (default: the block table's slots, bt[t / 64] * 64 + t % 64).
+    out: an int32 [rows, 2048] contiguous tensor to fill instead of a new one."""
+    if page_table_1 is None:
+        t = torch.arange(width, dtype=torch.int64, device=block_table.device)
+        page_table_1 = (block_table.long()[t // 64] * 64 + t % 64).to(torch.int32)
+    budget = _PREFILL_BUDGET if memory_budget_bytes is None else int(memory_budget_bytes)
+    cap = _PREFILL_MAX_SLAB_ROWS if max_slab_rows is None else int(max_slab_rows)
+    splits = _TOPK_SPLITS if _TOPK_IMPL == "split" else 1
+    return _C.prefill_indexer(q, weights, kv_cache, block_table, lens, width, page_table_1, budget, cap, splits, out)

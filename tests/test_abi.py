@@ -29,7 +29,8 @@ def test_header_declares_the_path():
     names = declared_functions()
     for n in ["dsa_dequant_k_paged", "dsa_gather_k_paged", "dsa_dequant_mla_paged", "dsa_quant_q_fp8",
               "dsa_store_k_cache", "dsa_mqa_logits_decode", "dsa_mqa_logits_prefill", "dsa_topk_workspace_bytes",
-              "dsa_topk_transform", "dsa_topk_transform_pre", "dsa_last_error", "dsa_device_cu_count"]:
+              "dsa_topk_transform", "dsa_topk_transform_pre", "dsa_topk_split_count", "dsa_prefill_slab_rows",
+              "dsa_prefill_indexer_workspace_bytes", "dsa_prefill_indexer", "dsa_last_error", "dsa_device_cu_count"]:
         assert n in names
 
 
@@ -101,3 +102,36 @@ def test_torch_bind_rejects_bad_operands():
                                             torch.zeros(2, 48), 1)
     assert not hcu_ops.mqa_logits_supported(q, kv, w, 1, block_table=torch.zeros(2, 4, dtype=torch.int32),
                                             max_context_len=300)
+
+
+def test_prefill_slab_policy(lib):
+    """Slab rows for a byte budget: a multiple of 8 rows when at least 8 fit, capped at the cap and
+    at the rows; the workspace holds one slab of f32 logits (256-B aligned) plus the top-k's."""
+    I64, I = ctypes.c_int64, ctypes.c_int
+    lib.dsa_prefill_slab_rows.argtypes = [I64, I64, I64, I64]
+    lib.dsa_prefill_slab_rows.restype = I64
+    lib.dsa_prefill_indexer_workspace_bytes.argtypes = [I64, I64, I64, I, I]
+    lib.dsa_prefill_indexer_workspace_bytes.restype = ctypes.c_size_t
+    width = 147456
+    assert lib.dsa_prefill_slab_rows(16384, width, 4096, 2 << 30) == 3640  # 2 GiB of logits rows
+    assert lib.dsa_prefill_slab_rows(16384, width, 4096, 4096 * width * 4) == 4096
+    assert lib.dsa_prefill_slab_rows(16384, width, 4096, 0) == 4096  # no budget: the cap
+    assert lib.dsa_prefill_slab_rows(5, width, 4096, 1 << 40) == 5
+    assert lib.dsa_prefill_slab_rows(100, width, 0, 13 * width * 4) == 8
+    assert lib.dsa_prefill_slab_rows(100, width, 0, 3 * width * 4) == 3
+    assert lib.dsa_prefill_slab_rows(100, width, 0, 1) == 1
+    need = lib.dsa_prefill_indexer_workspace_bytes(16384, width, 4096, 8, 256)
+    assert need == 4096 * width * 4  # 4096-row slabs: one CTA a row, no top-k workspace
+    small = lib.dsa_prefill_indexer_workspace_bytes(4, 70000, 4, 8, 256)
+    assert small > (4 * 70000 * 4 + 255) // 256 * 256  # four 70K rows split: the top-k's workspace too
+
+
+def test_reference_knob_gate(monkeypatch):
+    """mqa_logits pairs with the top-k only where the reference's gate would: the split top-k
+    must split rows (reference hcu_ops/hcu_ops/__init__.py:96-98).  MI355X: 256 CUs."""
+    import hcu_ops
+    monkeypatch.setattr(hcu_ops, "_N_CU", 256)
+    assert hcu_ops._topk_splits(128, 65536) > 1
+    assert hcu_ops._topk_splits(32, 16384) == 1
+    assert hcu_ops._topk_splits(1, 4096) == 1
+    assert hcu_ops._topk_splits(600, 65536) == 1

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import hcu_ops
-from hcu_ops import workloads as wl
+import workloads as wl
 from oracle import indexer as O
 
 from gpu_util import kv_np, q_bits

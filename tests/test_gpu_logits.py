@@ -6,8 +6,9 @@ import pytest
 import torch
 
 import hcu_ops
-from hcu_ops import workloads as wl
+import workloads as wl
 from oracle import indexer as O
+from oracle.topk_c import topk_radix
 
 from gpu_util import check_logits, kv_np, oracle_decode, oracle_q
 
@@ -83,20 +84,47 @@ def test_decode_logits_sparse_and_negative_modes(gpu):
     _check_decode(case, lg, mask)
 
 
-@pytest.mark.parametrize("group,lens", [(1, [9000, 5000, 1500, 40000]), (2, [20000, 3000]),
-                                        (2, [65536, 64000, 700, 0, 3000, 2049])])
-def test_decode_fused_histogram(gpu, monkeypatch, group, lens):
-    monkeypatch.setattr(hcu_ops, "_MQA_FUSED_PASS1", True)
+@pytest.mark.parametrize("group,lens,rpc", [(1, [9000, 5000, 1500, 40000], 1), (2, [20000, 3000], 2),
+                                            (2, [65536, 64000, 700, 0, 3000, 2049], 1),
+                                            (6, [30000, 2100], 3)])
+def test_decode_fused_histogram_reference_contract(gpu, group, lens, rpc):
+    """_C.mqa_logits_hist called with the reference's ten arguments (hcu_ops/csrc/bind.cpp:36-44)
+    and hist_lens leaves pass 1 in zws, checked as the reference's own test does
+    (hcu_ops/tests/test_mqa_hist.py:166-174, ok_h): ghist1 and (positives, zeros) equal the
+    closed form of test_mqa_hist.py:109-124 on the kernel's own logits, the second block is all
+    zero; then _C.sparse_mask_topk_transform_split_pre with the reference's eight arguments
+    consumes it and selects the oracle's set."""
+    from hcu_ops import _C
     case = wl.decode_case(13, lens, group=group, heads=64)
-    _, _, lg, mask = _run_decode(case, gpu, hist=True)
-    zws = hcu_ops._MQA_HIST[2].cpu().numpy() if hcu_ops._MQA_HIST is not None else None
-    assert zws is not None, "fused histogram not requested"
-    lens_np = case.context_lens.numpy()
-    ref = O.pass1_hist(lg.cpu().numpy(), mask.cpu().numpy(), lens_np, case.width)
-    B = case.rows
-    assert np.array_equal(zws[:B * 4096], ref[:B * 4096]), "ghist1 differs"
-    assert np.array_equal(zws[2 * B * 4096:], ref[2 * B * 4096:]), "(positives, zeros) differ"
-    assert not zws[B * 4096:2 * B * 4096].reshape(B, 4096)[:, :3].any(), "split counters not zeroed"
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    lens_d = case.context_lens.to(gpu)
+    B, W = case.rows, case.width
+    lg, mask, zws = _C.mqa_logits_hist(q8.unsqueeze(1), case.kv.to(gpu), w, lens_d, case.block_table.to(gpu), W,
+                                       group, 0, rpc, lens_d)
+    z = zws.cpu().numpy()
+    ref = O.pass1_hist(lg.cpu().numpy(), mask.cpu().numpy(), case.context_lens.numpy(), W)
+    assert np.array_equal(z[:B * 4096], ref[:B * 4096]), "ghist1 differs"
+    assert np.array_equal(z[2 * B * 4096:], ref[2 * B * 4096:]), "(positives, zeros) differ"
+    assert not z[B * 4096:2 * B * 4096].any(), "second histogram block not all zero"
+    _check_decode(case, lg, mask)
+    pt = case.page_table_1()
+    cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
+    got = _C.sparse_mask_topk_transform_split_pre(lg, mask, lens_d, pt.to(gpu), cu, 2048, 8, zws)
+    want = topk_radix(lg.cpu().numpy(), mask.cpu().numpy(), case.context_lens.numpy(), pt.numpy(), W)
+    assert np.array_equal(np.sort(got.cpu().numpy(), 1), np.sort(want, 1))
+
+
+def test_decode_logits_reference_arguments_reject_fused_r4(gpu):
+    """The fused pass 1 keeps 8 KB of LDS counters per row: rows_per_cta > 3 with hist_lens is
+    rejected unless fuse_pass1=False is passed (then only the counters are zeroed)."""
+    from hcu_ops import _C
+    case = wl.decode_case(15, [3000, 2500], group=4, heads=64)
+    q8, w = hcu_ops.quant_q_fp8(case.q.to(gpu), case.w.to(gpu))
+    lens_d = case.context_lens.to(gpu)
+    args = (q8.unsqueeze(1), case.kv.to(gpu), w, lens_d, case.block_table.to(gpu), case.width, 4, 0, 4, lens_d)
+    with pytest.raises(RuntimeError, match="rows_per_cta <= 3"):
+        _C.mqa_logits_hist(*args)
+    lg, mask, zws = _C.mqa_logits_hist(*args, fuse_pass1=False)
     _check_decode(case, lg, mask)
 
 

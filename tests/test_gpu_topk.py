@@ -8,7 +8,7 @@ import torch
 
 import hcu_ops
 from hcu_ops import _C
-from hcu_ops import workloads as wl
+import workloads as wl
 from oracle import indexer as O
 from oracle.topk_c import topk_radix
 
@@ -87,12 +87,13 @@ def test_topk_dense_and_varlen(gpu):
 
 
 @pytest.mark.parametrize("fused", [False, True])
-@pytest.mark.parametrize("group,lens", [(1, [30000, 12000, 4000, 1000]), (2, [65536, 60000, 3000, 2100, 900, 20000])])
+@pytest.mark.parametrize("group,lens", [(1, [40000, 12000, 4000, 1000]), (2, [65536, 60000, 3000, 2100, 900, 20000])])
 def test_topk_pass1_pairing(gpu, monkeypatch, fused, group, lens):
     """mqa_logits(hist_lens=lengths) -> sparse_mask_topk_transform consumes the paired pass-1
     workspace (zeroed by the logits call, or filled by it when fused) and gives the same set as
     the top-k with its own pass 1 on the same logits."""
-    monkeypatch.setattr(hcu_ops, "_MQA_FUSED_PASS1", fused)
+    monkeypatch.setattr(hcu_ops, "_MQA_HIST_MAX_ROWS", 1000 if fused else 0)
+    monkeypatch.setattr(hcu_ops, "_MQA_HIST_MAX_ROWS_G6", 1000 if fused else 0)
     case = wl.decode_case(17, lens, group=group, heads=64)
     gl = lambda t: t.to(gpu)
     q8, w = hcu_ops.quant_q_fp8(gl(case.q), gl(case.w))

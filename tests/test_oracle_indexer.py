@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from hcu_ops import workloads as wl
+import workloads as wl
 from oracle import indexer as O
 from oracle.fp8 import bf16_rne, float_key, fp8_decode
 from oracle.topk_c import topk_radix
