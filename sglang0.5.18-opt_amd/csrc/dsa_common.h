@@ -176,6 +176,25 @@ __device__ __forceinline__ int wave_prefix_5(int c, int& total) {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Block-wide (NT threads) exclusive prefix (thread order) and total of a per-thread count; one
+// barrier; s_w (NT / 64 words) must not be reused before the next barrier.
+template <int NT>
+__device__ __forceinline__ int block_excl_sum(int x, int& total, int* s_w) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int inc = wave_prefix_sum(x);
+  if (lane == 63) s_w[w] = inc;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int v = 0; v < NT / kWave; ++v) {
+    before += v < w ? s_w[v] : 0;
+    tot += s_w[v];
+  }
+  total = tot;
+  return before + inc - x;
+}
+
 // Slot of this lane among the active lanes of its wave with `pred` set, from one atomic add of
 // their count on *ctr (LDS or global) by the lowest of them.  Lanes without pred get a value
 // they must not use.  Replaces one same-address atomic per lane, which the LDS serialises.
@@ -188,6 +207,17 @@ __device__ __forceinline__ int wave_slot(bool pred, int* ctr) {
     base = __builtin_amdgcn_readlane(base, leader);
   }
   return base + lanes_below(m);
+}
+
+// The first of c (0 .. 31) consecutive slots for this lane, the lanes' slots in lane order after
+// one atomic add of the wave's total on *ctr (LDS or global) by lane 0.  Every lane of the wave
+// must call it.
+__device__ __forceinline__ int wave_slot_n(int c, int* ctr) {
+  int total;
+  const int before = wave_prefix_5(c, total);
+  int base = 0;
+  if (total != 0 && lane_id() == 0) base = atomicAdd(ctr, total);
+  return uniform(base) + before;
 }
 
 // max(x, +0) as one integer max on the float bits: negative floats (and -0.0) are negative

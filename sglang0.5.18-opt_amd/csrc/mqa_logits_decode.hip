@@ -135,25 +135,6 @@ __device__ __forceinline__ int group_ctas(int pages, int total_pages, int target
   return static_cast<int>((static_cast<int64_t>(pages) * target + total_pages - 1) / total_pages);
 }
 
-// Block-wide (NT threads) sum and exclusive prefix; s_w (NT / 64 words) must not be reused
-// before the next barrier.
-template <int NT>
-__device__ __forceinline__ int block_excl(int x, int& total, int* s_w) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int inc = wave_prefix_sum(x);
-  if (lane == 63) s_w[w] = inc;
-  __syncthreads();
-  int before = 0, tot = 0;
-#pragma unroll
-  for (int v = 0; v < NT / kWave; ++v) {
-    before += v < w ? s_w[v] : 0;
-    tot += s_w[v];
-  }
-  total = tot;
-  return before + inc - x;
-}
-
 // Work assignment, identical in every CTA: s_assign = {group (-1: none), index among the group's
 // CTAs, their count}; group g gets ceil(pages_g * T / P) CTAs.  Ends before a barrier (the caller's).
 template <int NT>
@@ -179,7 +160,7 @@ __device__ void assign_cta(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* 
     for (int g = g_lo; g < g_hi; ++g) my_pages += group_pages(a, g);
   }
   int total_pages;
-  block_excl<NT>(my_pages, total_pages, s_w[0]);
+  block_excl_sum<NT>(my_pages, total_pages, s_w[0]);
   if (tid == 0) s_assign[0] = -1;
   int my_ctas = 0;
   if (cached) {
@@ -189,7 +170,7 @@ __device__ void assign_cta(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* 
     for (int g = g_lo; g < g_hi; ++g) my_ctas += group_ctas(group_pages(a, g), total_pages, a.target);
   }
   int total_ctas;
-  int c0 = block_excl<NT>(my_ctas, total_ctas, s_w[1]);
+  int c0 = block_excl_sum<NT>(my_ctas, total_ctas, s_w[1]);
   if (cta >= c0 && cta < c0 + my_ctas) {
     for (int i = 0; g_lo + i < g_hi; ++i) {
       int p;

@@ -2,8 +2,10 @@
 //
 // Contract (hcu_ops/csrc/sparse_mask_topk.cu:1-22,141-349): per row, the 2048 tokens t < len
 // with the largest keys, ties at the threshold to the lower t; masked-out tokens are +0;
-// rows with len <= 2048 copy page_table[0:len] and pad with -1.  Only the set is the contract
-// (the order within a row is unspecified here, as it differs between the reference's variants).
+// rows with len <= 2048 copy page_table[0:len] and pad with -1.  Output order: the reference
+// single kernel's (sparse_mask_topk.cu:301-345), every token with key > thr in ascending token
+// order, then the ties taken in ascending token order -- a function of the scores alone, so
+// the layout is the same on every run and every graph replay.
 //
 // Algorithm (this file's own).  Default path, one read of the row: a fixed sample of the row
 // (256 chunks of 16 tokens, or the whole row up to 4096 tokens) gives a key K* that leaves, with
@@ -11,18 +13,19 @@
 // unordered pass collects them (positions from wave-aggregated LDS atomics, no barriers in the
 // streaming loop); they are resolved exactly by a 12-bit histogram of a digit relative to K*
 // (sized from the sample so that the threshold digit holds a handful of keys) and an exact
-// (key desc, token asc) rank of that digit's members.  If the count misses [2048, capacity] the
-// row takes the exact path, so the result never depends on the sample.
+// (key desc, token asc) rank of that digit's members; the selected tokens are then put in order
+// by a bitmap of the row's tokens and a prefix count of its words (emit_sorted).  If the count
+// misses [2048, capacity] the row takes the exact path, so the result never depends on the sample.
 // Exact path (radix digits 12/12/8 of the 32-bit key):
 //   pass 1   histogram of key[31:20] over the nonzero tokens plus positive / zero counts (or
 //            taken from the logits kernel).  positives <= 2048 <= positives + zeros means the
 //            threshold is +0 (sparse fast path).  Otherwise the threshold digit t1 follows.
-//   collect  one unordered pass over the row: tokens above bin t1 (or positive, fast path) are
-//            written straight to the output, tokens in bin t1 become candidates (key, token).
-//   resolve  the candidates (in LDS) go through the remaining digit passes to the exact
-//            threshold key and the number of threshold ties to take (the lowest indices).  Fast
-//            path: the first zeros come from an ordered scan of the row's prefix.
-//   overflow candidates that do not fit in LDS are resolved by re-reading the row.
+//   collect  one unordered pass over the row: tokens in bin t1 become candidates (key, token).
+//   select   the candidates (in LDS) go through the remaining digit passes to the exact
+//            threshold key and the number of threshold ties to take; candidates that do not fit
+//            in LDS are resolved by re-reading the row.
+//   emit     an ordered pass over the row writes the tokens above the threshold and the first
+//            ties (emit_row).
 // Few rows: S CTAs per row collect one slice each and publish their candidates through per-row
 // global counters; the last CTA of the row to finish (device-scope atomic) resolves them.
 // Many rows: one CTA per row does everything.  No host synchronisation; launch shapes depend
@@ -107,13 +110,13 @@ __device__ __forceinline__ int block_sum(int x, int* s_red) {
   return s;
 }
 
-// Block-exclusive prefix (thread order) of a per-thread count in [0, 7]; one barrier, with the
-// wave totals double-buffered by `parity` so back-to-back calls do not race.
-template <int NT>
+// Block-exclusive prefix (thread order) of a per-thread count in [0, 7] (kWide: [0, 31]); one
+// barrier, with the wave totals double-buffered by `parity` so back-to-back calls do not race.
+template <int NT, bool kWide = false>
 __device__ __forceinline__ int block_prefix(int c, int& total, int* s_scan, int parity) {
   constexpr int W = NT / kWave;
   int wt;
-  const int x = wave_prefix_small(c, wt);
+  const int x = kWide ? wave_prefix_5(c, wt) : wave_prefix_small(c, wt);
   const int w = threadIdx.x >> 6;
   int* buf = s_scan + parity * W;
   if (lane_id() == 0) buf[w] = wt;
@@ -133,7 +136,7 @@ __device__ __forceinline__ int block_prefix(int c, int& total, int* s_scan, int 
 // suffix(t + 1), count of t} ({0, 0, 0} if the histogram holds fewer than need[i], which
 // consistent inputs never do).  Ends with a barrier.
 template <int NT, int BPT, int NN>
-__device__ void find_thresholds_regs(const int (&h)[BPT], const int (&need)[NN], int* s_wtot, int* s_res) {
+__device__ __forceinline__ void find_thresholds_regs(const int (&h)[BPT], const int (&need)[NN], int* s_wtot, int* s_res) {
   constexpr int W = NT / kWave;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -170,14 +173,14 @@ __device__ void find_thresholds_regs(const int (&h)[BPT], const int (&need)[NN],
 }
 
 template <int NT, int BPT>
-__device__ void find_threshold_regs(const int (&h)[BPT], int need, int* s_wtot, int* s_res) {
+__device__ __forceinline__ void find_threshold_regs(const int (&h)[BPT], int need, int* s_wtot, int* s_res) {
   const int n[1] = {need};
   find_thresholds_regs<NT, BPT, 1>(h, n, s_wtot, s_res);
 }
 
 // The same over an LDS histogram of NB bins.
 template <int NB, int NT, int NN>
-__device__ void find_thresholds(const int* hist, const int (&need)[NN], int* s_wtot, int* s_res) {
+__device__ __forceinline__ void find_thresholds(const int* hist, const int (&need)[NN], int* s_wtot, int* s_res) {
   constexpr int BPT = NB >= NT ? NB / NT : 1;
   constexpr int ACTIVE = NB / BPT;
   int h[BPT];
@@ -187,7 +190,7 @@ __device__ void find_thresholds(const int* hist, const int (&need)[NN], int* s_w
 }
 
 template <int NB, int NT>
-__device__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_res) {
+__device__ __forceinline__ void find_threshold(const int* hist, int need, int* s_wtot, int* s_res) {
   const int n[1] = {need};
   find_thresholds<NB, NT, 1>(hist, n, s_wtot, s_res);
 }
@@ -233,7 +236,7 @@ struct Meta {
 };
 
 template <int NT>
-__device__ Meta row_meta(const int* hist_lds, int pos, int zeros, int* s_wtot, int* s_res) {
+__device__ __forceinline__ Meta row_meta(const int* hist_lds, int pos, int zeros, int* s_wtot, int* s_res) {
   Meta m;
   m.pos = pos;
   m.fast = pos <= kTopK && pos + zeros >= kTopK;
@@ -278,7 +281,7 @@ __device__ __forceinline__ void stream_batches(const RowSrc& rr, int b, int n_ba
 // Pass 1 over [begin, end) (end > begin) of the row into the LDS histogram `hist` (zeroed here;
 // zeros counted, not binned); returns the range's positive / zero counts (block-uniform).
 template <bool kVec, int NT>
-__device__ void pass_hist(const RowSrc& r, int begin, int end, int* hist, int* s_red, int& pos, int& zeros) {
+__device__ __forceinline__ void pass_hist(const RowSrc& r, int begin, int end, int* hist, int* s_red, int& pos, int& zeros) {
   constexpr int kStep = NT * 4 * kUnroll;
   RowSrc rr = r;
   rr.len = end;
@@ -311,76 +314,49 @@ __device__ void pass_hist(const RowSrc& r, int begin, int end, int* hist, int* s
   zeros = block_sum<NT>(zc, s_red);
 }
 
-// Candidate staging of a CTA: certain tokens (A) and threshold-bin candidates (C).
-struct Stage {
-  int* a;         // token indices, capacity cap_a
-  uint32_t* ck;   // candidate keys, capacity cap_c
-  int* ci;        // candidate tokens
-  int* n_a;       // LDS counters
-  int* n_c;
-  int cap_a;
-  int cap_c;
-};
-
-// A = keys above bin t1 (fast path: positive keys), C = keys in bin t1 (none on the fast
-// path).  A lane flags its (at most 16) hits of the batch in two bitmasks; one wave prefix per
-// list and one wave-aggregated LDS atomic per list and batch give every hit its staging slot.
+// Candidates of the threshold bin: the keys of a batch whose 12-bit digit key[31:20] is t1 go to
+// the LDS list (ck, ci) at slots from one wave-aggregated atomic per batch; the count keeps
+// growing past cap (the caller sees the overflow), the stores stop at cap.
 template <int NT>
-__device__ __forceinline__ void process_batch(const RowSrc& rr, int b, const Batch& x, const Meta& m,
-                                              const Stage& st) {
+__device__ __forceinline__ void process_bin(const RowSrc& rr, int b, const Batch& x, uint32_t t1, uint32_t* ck,
+                                            int* ci, int* n, int cap) {
   static_assert(kUnroll * 4 <= 16, "hit masks hold 16 keys");
   uint32_t k[kUnroll][4];
-  uint32_t fa = 0, fc = 0;
+  uint32_t f = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const uint32_t v = quad_keys(rr, b + u * NT * 4, x.q[u], k[u]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool valid = (v >> j) & 1u;
-      const uint32_t d = k[u][j] >> 20;
-      fa |= static_cast<uint32_t>(valid && (m.fast ? k[u][j] > kZeroKey : d > m.t1)) << (u * 4 + j);
-      fc |= static_cast<uint32_t>(valid && !m.fast && d == m.t1) << (u * 4 + j);
-    }
+    for (int j = 0; j < 4; ++j) f |= static_cast<uint32_t>(((v >> j) & 1u) && (k[u][j] >> 20) == t1) << (u * 4 + j);
   }
-  int ta, tc;
-  int pa = wave_prefix_5(__popc(fa), ta);
-  int pc = wave_prefix_5(__popc(fc), tc);
-  if ((ta | tc) == 0) return;  // wave-uniform
-  int base_a = 0, base_c = 0;
-  if (lane_id() == 0) {
-    if (ta) base_a = atomicAdd(st.n_a, ta);
-    if (tc) base_c = atomicAdd(st.n_c, tc);
-  }
-  pa += uniform(base_a);
-  pc += uniform(base_c);
+  int t;
+  int p = wave_prefix_5(__popc(f), t);
+  if (t == 0) return;  // wave-uniform
+  int base = 0;
+  if (lane_id() == 0) base = atomicAdd(n, t);
+  p += uniform(base);
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int e = u * 4 + j;
-      const int t = b + u * NT * 4 + j;
-      if ((fa >> e) & 1u) {
-        if (pa < st.cap_a) st.a[pa] = t;
-        ++pa;
-      }
-      if ((fc >> e) & 1u) {
-        if (pc < st.cap_c) {
-          st.ck[pc] = k[u][j];
-          st.ci[pc] = t;
+      if ((f >> (u * 4 + j)) & 1u) {
+        if (p < cap) {
+          ck[p] = k[u][j];
+          ci[p] = b + u * NT * 4 + j;
         }
-        ++pc;
+        ++p;
       }
     }
   }
 }
 
-// Unordered collection of n_batches batches from lane offset b (x0 / x1: the first two, already
-// issued).  Loads past rr.len are redirected inside the row and masked off.
+// Unordered collection of the bin-t1 keys of n_batches batches from lane offset b (x0 / x1: the
+// first two, already issued).  Loads past rr.len are redirected inside the row and masked off.
 template <bool kVec, int NT>
-__device__ void collect(const RowSrc& rr, int b, int n_batches, const Meta& m, const Stage& st, Batch& x0,
-                        Batch& x1) {
+__device__ __forceinline__ void collect_bin(const RowSrc& rr, int b, int n_batches, uint32_t t1, uint32_t* ck, int* ci, int* n,
+                            int cap, Batch& x0, Batch& x1) {
   stream_batches<kVec, NT>(rr, b, n_batches, x0, x1,
-                           [&](int bb, const Batch& x) { process_batch<NT>(rr, bb, x, m, st); });
+                           [&](int bb, const Batch& x) { process_bin<NT>(rr, bb, x, t1, ck, ci, n, cap); });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -468,7 +444,7 @@ __device__ __forceinline__ void sample_issue(const RowSrc& r, SampleLoads<NT>& x
 // K* of row r and the candidate digit from its issued sample (block-uniform; every CTA of the
 // row computes the same).
 template <int NT>
-__device__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x, const SampleLds& S) {
+__device__ __forceinline__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x, const SampleLds& S) {
   constexpr int QPT = SampleLoads<NT>::QPT;
   const int tid = threadIdx.x;
   const Quad* q = x.q;
@@ -564,7 +540,7 @@ __device__ __forceinline__ void process_ge(const RowSrc& rr, int b, const Batch&
 }
 
 template <bool kVec, int NT>
-__device__ void collect_ge(const RowSrc& rr, int b, int n_batches, uint32_t thr, uint32_t* ck, int* ci, int* n,
+__device__ __forceinline__ void collect_ge(const RowSrc& rr, int b, int n_batches, uint32_t thr, uint32_t* ck, int* ci, int* n,
                            int cap, Batch& x0, Batch& x1) {
   if (thr >= kZeroKey) {  // block-uniform
     stream_batches<kVec, NT>(rr, b, n_batches, x0, x1, [&](int bb, const Batch& x) {
@@ -581,7 +557,7 @@ __device__ void collect_ge(const RowSrc& rr, int b, int n_batches, uint32_t thr,
 // number of members with key > thr (returned in above).  key_of(e) / member(e) index 0..n-1.
 // d1_known >= 0: every member's key[31:20] is d1_known (the first digit pass is skipped).
 template <int NT, typename KeyOf, typename Member>
-__device__ uint32_t radix_select(int n, int need, KeyOf key_of, Member member, int* hist, int* s_wtot, int* s_res,
+__device__ __forceinline__ uint32_t radix_select(int n, int need, KeyOf key_of, Member member, int* hist, int* s_wtot, int* s_res,
                                  int& above, int d1_known = -1) {
   uint32_t d1;
   int ab = 0;
@@ -625,7 +601,7 @@ __device__ uint32_t radix_select(int n, int need, KeyOf key_of, Member member, i
 }
 
 template <int NT, int CAP>
-struct ResolveLds {
+struct alignas(16) ResolveLds {  // 16-B LDS accesses into hist, ck and ci
   int hist[kBins];
   uint32_t ck[CAP];
   int ci[CAP];
@@ -633,279 +609,25 @@ struct ResolveLds {
   int wtot[NT / kWave];
   int red[NT / kWave];
   int res[6];
-  int misc[4];
+  int misc[8];
 };
 
-// Resolves the LDS candidates (unordered) of a row whose above1 tokens above them are already in
-// dst[0, above1): radix passes over the key (the first skipped when all share key[31:20] = d1
-// >= 0), then the ties at the threshold key, lowest tokens first.  The general path of
-// resolve_lds and resolve_cands.
+// The threshold of a row from its candidates in LDS (L.ck, n of them, all of 12-bit digit d1,
+// or d1 < 0: unknown) of which `need` are to be taken: the key thr of the need-th largest and
+// the number of ties at thr among them (taken from the lowest tokens).
 template <int NT, int CAP>
-__device__ void resolve_lds_radix(ResolveLds<NT, CAP>& L, int n_c, int d1, int above1, const PtRow& pt,
-                                  int32_t* dst) {
-  const int need1 = kTopK - above1;
+__device__ __forceinline__ uint32_t select_lds(ResolveLds<NT, CAP>& L, int n, int d1, int need, int& remaining) {
   int gt;
   const uint32_t thr = radix_select<NT>(
-      n_c, need1, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt, d1);
-  const int remaining = need1 - gt;
-  const int tie_base = kTopK - remaining;
-  // ties at thr: all of them, unless there are more than `remaining` -- then the lowest tokens,
-  // found by a radix select over ~token among the ties.
-  int n_eq = 0;
-  for (int e = threadIdx.x; e < n_c; e += NT) n_eq += L.ck[e] == thr;
-  n_eq = block_sum<NT>(n_eq, L.red);
-  uint32_t idx_thr = 0;  // ties kept: ~token >= idx_thr
-  if (n_eq > remaining) {
-    int unused;
-    idx_thr = radix_select<NT>(
-        n_c, remaining, [&](int e) { return ~static_cast<uint32_t>(L.ci[e]); },
-        [&](int e) { return L.ck[e] == thr; }, L.hist, L.wtot, L.res, unused);
-  }
-  int gt_pos = 0, tie_pos = 0, parity = 0;
-  for (int base = 0; base < n_c; base += NT) {
-    const int e = base + static_cast<int>(threadIdx.x);
-    const uint32_t key = e < n_c ? L.ck[e] : 0u;
-    const bool g = e < n_c && key > thr;
-    const bool q = e < n_c && key == thr && ~static_cast<uint32_t>(L.ci[e]) >= idx_thr;
-    int tg, tq;
-    const int pg = block_prefix<NT>(g, tg, L.scan, parity);
-    parity ^= 1;
-    const int pq = block_prefix<NT>(q, tq, L.scan, parity);
-    parity ^= 1;
-    if (g) put(dst, above1 + gt_pos + pg, pt[L.ci[e]]);
-    if (q) put(dst, tie_base + tie_pos + pq, pt[L.ci[e]]);
-    gt_pos += tg;
-    tie_pos += tq;
-  }
+      n, need, [&](int e) { return L.ck[e]; }, [](int) { return true; }, L.hist, L.wtot, L.res, gt, d1);
+  remaining = need - gt;
+  return thr;
 }
 
-// Resolves the LDS candidates (all in bin t1, unordered, n_c of them) of a row whose above1
-// tokens above bin t1 are already in dst[0, above1).  One digit pass over key[19:8] splits them
-// into certain ones (digit above the threshold digit d2, emitted at once) and the members of
-// digit d2, which are few for any spread of values: each member's exact rank in (key desc,
-// token asc) order decides it.  More members than threads (heavy ties) take the radix path.
-template <int NT, int CAP>
-__device__ void resolve_lds(ResolveLds<NT, CAP>& L, int n_c, uint32_t t1, int above1, const PtRow& pt, int32_t* dst) {
-  const int need1 = kTopK - above1;
-  zero_lds<NT>(L.hist, kBins);
-  if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
-  __syncthreads();
-  for (int e = threadIdx.x; e < n_c; e += NT) atomicAdd(&L.hist[(L.ck[e] >> 8) & 0xFFFu], 1);
-  __syncthreads();
-  find_threshold<kBins, NT>(L.hist, need1, L.wtot, L.res);
-  const uint32_t d2 = static_cast<uint32_t>(L.res[0]);
-  const int above2 = L.res[1];
-  const int n2 = L.res[2];
-  if (n2 > NT) {  // block-uniform
-    resolve_lds_radix(L, n_c, static_cast<int>(t1), above1, pt, dst);
-    return;
-  }
-  const int need2 = need1 - above2;  // members to take
-  // the histogram is consumed: its first 2 * NT words hold the members' keys and tokens
-  uint32_t* mk = reinterpret_cast<uint32_t*>(L.hist);
-  int* mt = L.hist + NT;
-  for (int base = 0; base < n_c; base += NT) {  // block-uniform trip count
-    const int e = base + static_cast<int>(threadIdx.x);
-    const bool in = e < n_c;
-    const uint32_t k = in ? L.ck[e] : 0u;
-    const int tok = in ? L.ci[e] : 0;
-    const uint32_t d = (k >> 8) & 0xFFFu;
-    const bool ga = in && d > d2;
-    const bool gm = in && d == d2;
-    const int sa = wave_slot(ga, &L.misc[0]);
-    const int sm = wave_slot(gm, &L.misc[1]);
-    if (ga) put(dst, above1 + sa, pt[tok]);
-    if (gm && sm < NT) {
-      mk[sm] = k;
-      mt[sm] = tok;
-    }
-  }
-  __syncthreads();
-  const int t = threadIdx.x;
-  if (t < n2) {
-    const uint32_t k = mk[t];
-    const int tok = mt[t];
-    int rank = 0;
-    int j = 0;
-#pragma unroll 4
-    for (; j + 4 <= n2; j += 4) {  // 16-B LDS reads (mk and mt are 16-B aligned)
-      const uint4 kj = *reinterpret_cast<const uint4*>(mk + j);
-      const int4 tj = *reinterpret_cast<const int4*>(mt + j);
-      rank += (kj.x > k || (kj.x == k && tj.x < tok)) + (kj.y > k || (kj.y == k && tj.y < tok)) +
-              (kj.z > k || (kj.z == k && tj.z < tok)) + (kj.w > k || (kj.w == k && tj.w < tok));
-    }
-    for (; j < n2; ++j) rank += mk[j] > k || (mk[j] == k && mt[j] < tok);
-    if (rank < need2) put(dst, kTopK - need2 + rank, pt[tok]);
-  }
-}
-
-// Resolves n (kTopK <= n <= CAP) collected candidates (keys >= cut.thr) that hold the row's top
-// 2048; load(e, k, t) fetches candidate e (from LDS, or from the row's published list).  A
-// histogram of their digit cand_digit gives the threshold digit t1: candidates above it go
-// straight to the output, its members are ranked exactly by (key desc, token asc) -- a handful
-// by the choice of the digit -- or, when there are more than NT, resolved by radix passes.
-template <int NT, int CAP, typename Load>
-__device__ void resolve_cands(ResolveLds<NT, CAP>& L, int n, const SampleCut& cut, const PtRow& pt, int32_t* dst,
-                              Load load) {
-  constexpr int EPT = CAP / NT;
-  static_assert(EPT * NT == CAP, "candidates split over the block");
-  const int tid = threadIdx.x;
-  uint32_t kk[EPT];
-  int tt[EPT];
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {  // every load in flight before the first use
-    const int e = tid + j * NT;
-    kk[j] = 0u;
-    tt[j] = 0;
-    if (e < n) load(e, kk[j], tt[j]);
-  }
-  int32_t pv[EPT];  // page-table entries, fetched while the threshold is searched
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) pv[j] = tid + j * NT < n ? pt[tt[j]] : -1;
-  zero_lds<NT>(L.hist, kBins);
-  if (tid == 0) L.misc[0] = L.misc[1] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < EPT; ++j)
-    if (tid + j * NT < n) atomicAdd(&L.hist[cand_digit(kk[j], cut)], 1);
-  __syncthreads();
-  find_threshold<kBins, NT>(L.hist, kTopK, L.wtot, L.res);
-  const uint32_t t1 = static_cast<uint32_t>(L.res[0]);
-  const int above1 = L.res[1];
-  const int n_t1 = L.res[2];
-  const bool direct = n_t1 <= NT;  // block-uniform: members ranked directly, their entries in hist
-  static_assert(EPT <= 16, "masks hold 16 candidates");
-  uint32_t fa = 0, fm = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const bool in = tid + j * NT < n;
-    const uint32_t d = cand_digit(kk[j], cut);
-    fa |= static_cast<uint32_t>(in && d > t1) << j;
-    fm |= static_cast<uint32_t>(in && d == t1) << j;
-  }
-  {
-    int ta, tm;
-    int pa = wave_prefix_5(__popc(fa), ta);
-    int pm = wave_prefix_5(__popc(fm), tm);
-    int ba = 0, bm = 0;
-    if (lane_id() == 0) {
-      if (ta) ba = atomicAdd(&L.misc[0], ta);
-      if (tm) bm = atomicAdd(&L.misc[1], tm);
-    }
-    pa += uniform(ba);
-    pm += uniform(bm);
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      if ((fa >> j) & 1u) put(dst, pa++, pv[j]);
-      if ((fm >> j) & 1u) {
-        L.ck[pm] = kk[j];
-        L.ci[pm] = tt[j];
-        if (direct) L.hist[pm] = pv[j];
-        ++pm;
-      }
-    }
-  }
-  __syncthreads();
-  if (!direct) {
-    resolve_lds_radix(L, n_t1, -1, above1, pt, dst);
-    return;
-  }
-  const int need1 = kTopK - above1;
-  if (tid < n_t1) {
-    const uint32_t k = L.ck[tid];
-    const int tok = L.ci[tid];
-    int rank = 0;
-    int j = 0;
-#pragma unroll 4
-    for (; j + 4 <= n_t1; j += 4) {  // 16-B LDS reads (ck and ci are 16-B aligned)
-      const uint4 kj = *reinterpret_cast<const uint4*>(L.ck + j);
-      const int4 tj = *reinterpret_cast<const int4*>(L.ci + j);
-      rank += (kj.x > k || (kj.x == k && tj.x < tok)) + (kj.y > k || (kj.y == k && tj.y < tok)) +
-              (kj.z > k || (kj.z == k && tj.z < tok)) + (kj.w > k || (kj.w == k && tj.w < tok));
-    }
-    for (; j < n_t1; ++j) rank += L.ck[j] > k || (L.ck[j] == k && L.ci[j] < tok);
-    if (rank < need1) put(dst, above1 + rank, L.hist[tid]);
-  }
-}
-
-// A row of at most kSample tokens: every key goes to the candidate list at its token's
-// position (no threshold, no collection pass) and is resolved on the plain 12-bit digit.
+// The same by re-reading the row (its bin-t1 candidates did not fit in LDS): digit passes over
+// key[19:8], then key[7:0], of the row's tokens in bin t1.
 template <bool kVec, int NT, int CAP>
-__device__ void small_row(ResolveLds<NT, CAP>& L, const RowSrc& r, const PtRow& pt, int32_t* dst) {
-  static_assert(CAP >= kSample, "the row fits the candidate list");
-  constexpr int QPT = kSample / 4 / NT;
-#pragma unroll
-  for (int j = 0; j < QPT; ++j) {
-    const int i0 = (static_cast<int>(threadIdx.x) + j * NT) * 4;
-    Quad q;
-    load_quad<kVec>(r, i0, q);
-    uint32_t k[4];
-    const uint32_t v = quad_keys(r, i0, q, k);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if ((v >> e) & 1u) {
-        L.ck[i0 + e] = k[e];
-        L.ci[i0 + e] = i0 + e;
-      }
-    }
-  }
-  __syncthreads();
-  SampleCut cut;
-  cut.thr = 0u;
-  cut.shift = 20;
-  resolve_cands(L, r.len, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
-    k = L.ck[e];
-    t = L.ci[e];
-  });
-}
-
-// Ordered scan of the row for the first `remaining` tokens with key == thr that pass `cond`
-// (fast path: the zeros; rescan: the ties), written to dst[base + rank]; stops once enough
-// were found unless gt is set.  gt: also write the keys > thr that pass cond to
-// dst[gt_base + rank] (rescan only; then the whole row is scanned).
-template <bool kVec, int NT, typename Cond>
-__device__ void ordered_scan(const RowSrc& r, Cond cond, uint32_t thr, bool gt, int gt_base, int base, int remaining,
-                             const PtRow& pt, int32_t* dst, int* s_scan) {
-  int taken = 0, gt_pos = 0, parity = 0;
-  for (int b0 = 0; b0 < r.len && (gt || taken < remaining); b0 += NT * 4) {
-    const int i0 = b0 + static_cast<int>(threadIdx.x) * 4;
-    uint32_t k[4];
-    const uint32_t v = load_keys4<kVec>(r, i0, k);
-    int ne = 0, ng = 0;
-    bool e[4], g[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool c = ((v >> j) & 1u) && cond(k[j]);
-      e[j] = c && k[j] == thr;
-      g[j] = gt && c && k[j] > thr;
-      ne += e[j];
-      ng += g[j];
-    }
-    int te, tg;
-    int pe = block_prefix<NT>(ne, te, s_scan, parity);
-    parity ^= 1;
-    int pg = block_prefix<NT>(ng, tg, s_scan, parity);
-    parity ^= 1;
-    pe += taken;
-    pg += gt_pos;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (e[j] && pe < remaining) put(dst, base + pe, pt[i0 + j]);
-      if (g[j]) put(dst, gt_base + pg, pt[i0 + j]);
-      pe += e[j];
-      pg += g[j];
-    }
-    taken += te;
-    gt_pos += tg;
-  }
-}
-
-// Threshold resolution by re-reading the row (candidates did not fit in LDS): digit passes over
-// the tokens of bin t1, then an ordered emission of those above / at the threshold.
-template <bool kVec, int NT, int CAP>
-__device__ void resolve_rescan(ResolveLds<NT, CAP>& L, const RowSrc& r, uint32_t t1, int above1, const PtRow& pt,
-                               int32_t* dst) {
-  const int need1 = kTopK - above1;
+__device__ __forceinline__ uint32_t select_rescan(ResolveLds<NT, CAP>& L, const RowSrc& r, uint32_t t1, int need1, int& remaining) {
   zero_lds<NT>(L.hist, kBins);
   __syncthreads();
   for (int b = static_cast<int>(threadIdx.x) * 4; b < r.len; b += NT * 4) {
@@ -930,11 +652,339 @@ __device__ void resolve_rescan(ResolveLds<NT, CAP>& L, const RowSrc& r, uint32_t
   }
   __syncthreads();
   find_threshold<256, NT>(L.hist, need2, L.wtot, L.res);
-  const uint32_t thr = (prefix24 << 8) | static_cast<uint32_t>(L.res[0]);
-  const int remaining = need2 - L.res[1];
-  ordered_scan<kVec, NT>(
-      r, [t1](uint32_t k) { return (k >> 20) == t1; }, thr, true, above1, kTopK - remaining, remaining, pt, dst,
-      L.scan);
+  remaining = need2 - L.res[1];
+  return (prefix24 << 8) | static_cast<uint32_t>(L.res[0]);
+}
+
+// Ordered emission by one CTA streaming the row once more (the exact and heavy-tie paths): every
+// token with key > thr to dst[0, kTopK - remaining), the first `remaining` tokens with key ==
+// thr to dst[kTopK - remaining, kTopK), each part in ascending token order.  A thread owns 16
+// consecutive tokens of each 16 NT-token step (one block prefix per part and step); the next
+// step's scores are loaded before this step's prefixes.  Stops once both parts are complete.
+template <bool kVec, int NT>
+__device__ __forceinline__ void emit_row(const RowSrc& r, uint32_t thr, int remaining, const PtRow& pt, int32_t* dst, int* s_scan) {
+  constexpr int kStep = NT * 16;
+  const int tie_base = kTopK - remaining;
+  const int t0 = static_cast<int>(threadIdx.x) * 16;
+  int na = 0, nt = 0, parity = 0;
+  Quad cur[4], nxt[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) load_quad<kVec>(r, t0 + 4 * u, cur[u]);
+  for (int b = 0; b < r.len && (na < tie_base || nt < remaining); b += kStep) {  // block-uniform
+    const int i0 = b + t0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_quad<kVec>(r, i0 + kStep + 4 * u, nxt[u]);
+    uint32_t fa = 0, ft = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t k[4];
+      const uint32_t v = quad_keys(r, i0 + 4 * u, cur[u], k);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool valid = (v >> j) & 1u;
+        fa |= static_cast<uint32_t>(valid && k[j] > thr) << (4 * u + j);
+        ft |= static_cast<uint32_t>(valid && k[j] == thr) << (4 * u + j);
+      }
+    }
+    int ta, tt;
+    int pa = block_prefix<NT, true>(__popc(fa), ta, s_scan, parity);
+    parity ^= 1;
+    int pq = block_prefix<NT, true>(__popc(ft), tt, s_scan, parity);
+    parity ^= 1;
+    pa += na;
+    pq += nt;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if ((fa >> e) & 1u) put(dst, pa++, pt[i0 + e]);
+      if ((ft >> e) & 1u) {
+        if (pq < remaining) put(dst, tie_base + pq, pt[i0 + e]);
+        ++pq;
+      }
+    }
+    na += ta;
+    nt += tt;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+  }
+}
+
+// Ordered emission of a resolved selection held in an LDS list: sel[0, nA) the tokens with key >
+// thr, sel[kTopK - nT, kTopK) the ties taken (nA + nT == kTopK), each part in any order, val(i)
+// the page-table entry of sel[i].  Per window of kEmitWin tokens, a bitmap of each part's tokens
+// (`bits`, 4096 words: [0, 2048) the first part, [2048, 4096) the ties) and the prefix counts of
+// its words (`pre`) give every token its rank within its part, its slot dst[rank] (first part)
+// or dst[nA + rank] (ties).  Four barriers a window; one window covers a row of up to 64K tokens.
+constexpr int kEmitWords = kBins / 2;
+constexpr int kEmitWin = kEmitWords * 32;
+
+template <int NT, typename Val>
+__device__ __forceinline__ void emit_sorted(const int* sel, int nA, Val val, uint32_t* bits, uint16_t* pre, int* s_w, int len,
+                            int32_t* dst) {
+  constexpr int WPT = kBins / NT;  // words a thread zeroes and counts; all of one part
+  static_assert(WPT * NT == kBins && WPT % 4 == 0 && kEmitWords % WPT == 0, "bitmap split over the block");
+  const int tid = threadIdx.x;
+  int base_a = 0, base_t = nA;
+  for (int w0 = 0; w0 < len; w0 += kEmitWin) {  // block-uniform
+    uint4* b4 = reinterpret_cast<uint4*>(bits + tid * WPT);
+#pragma unroll
+    for (int j = 0; j < WPT / 4; ++j) b4[j] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    for (int i = tid; i < kTopK; i += NT) {
+      const int x = sel[i] - w0;
+      if (static_cast<unsigned>(x) < static_cast<unsigned>(kEmitWin))
+        atomicOr(&bits[(i < nA ? 0 : kEmitWords) + (x >> 5)], 1u << (x & 31));
+    }
+    __syncthreads();
+    int pc[WPT];
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < WPT / 4; ++j) {
+      const uint4 q = b4[j];
+      pc[4 * j] = c;
+      c += __popc(q.x);
+      pc[4 * j + 1] = c;
+      c += __popc(q.y);
+      pc[4 * j + 2] = c;
+      c += __popc(q.z);
+      pc[4 * j + 3] = c;
+      c += __popc(q.w);
+    }
+    int total;
+    int ex = block_excl_sum<NT>(c, total, s_w);
+    int tot_a = 0;  // the first part's count in this window: the words of threads [0, NT / 2)
+#pragma unroll
+    for (int v = 0; v < NT / kWave / 2; ++v) tot_a += s_w[v];
+    if (tid >= NT / 2) ex -= tot_a;
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) pre[tid * WPT + j] = static_cast<uint16_t>(ex + pc[j]);
+    __syncthreads();
+    for (int i = tid; i < kTopK; i += NT) {
+      const int x = sel[i] - w0;
+      if (static_cast<unsigned>(x) < static_cast<unsigned>(kEmitWin)) {
+        const int wd = (i < nA ? 0 : kEmitWords) + (x >> 5);
+        const int rank = pre[wd] + __popc(bits[wd] & ((1u << (x & 31)) - 1u));
+        put(dst, (i < nA ? base_a : base_t) + rank, val(i));
+      }
+    }
+    base_a += tot_a;
+    base_t += total - tot_a;
+    __syncthreads();
+  }
+}
+
+// The exact selection of one row by one CTA (the sampled kernels' fallback): pass-1 histogram;
+// sparse fast path (threshold +0); or collection of the threshold bin's candidates (up to CAP in
+// L.ck / L.ci), their threshold in LDS or by re-reading the row; then the ordered emission.
+template <bool kVec, int NT, int CAP>
+__device__ __forceinline__ void exact_row(ResolveLds<NT, CAP>& L, const RowSrc& r, const PtRow& pt, int32_t* dst) {
+  constexpr int kStep = NT * 4 * kUnroll;
+  int pos, zeros;
+  pass_hist<kVec, NT>(r, 0, r.len, L.hist, L.red, pos, zeros);
+  if (threadIdx.x == 0 && zeros) L.hist[kZeroBin] += zeros;
+  __syncthreads();
+  const Meta m = row_meta<NT>(L.hist, pos, zeros, L.wtot, L.res);
+  if (m.fast) {  // block-uniform
+    emit_row<kVec, NT>(r, kZeroKey, kTopK - m.pos, pt, dst, L.scan);
+    return;
+  }
+  const int b0 = static_cast<int>(threadIdx.x) * 4;
+  Batch x0, x1;
+  load_batch<kVec, NT>(r, b0, x0);
+  load_batch<kVec, NT>(r, b0 + kStep, x1);
+  if (threadIdx.x == 0) L.misc[1] = 0;
+  __syncthreads();
+  collect_bin<kVec, NT>(r, b0, (r.len + kStep - 1) / kStep, m.t1, L.ck, L.ci, &L.misc[1], CAP, x0, x1);
+  __syncthreads();
+  const int n_c = L.misc[1];
+  const int need1 = kTopK - m.above1;
+  int remaining;
+  const uint32_t thr = n_c <= CAP ? select_lds(L, n_c, static_cast<int>(m.t1), need1, remaining)
+                                  : select_rescan<kVec>(L, r, m.t1, need1, remaining);
+  emit_row<kVec, NT>(r, thr, remaining, pt, dst, L.scan);
+}
+
+// The reference takes the threshold +0, with no ties, whenever positives <= 2048 <= positives +
+// zeros (its sparse fast path, sparse_mask_topk.cu:199-234); that differs from the 2048th largest
+// key thr only when the row holds exactly 2048 positive keys -- then all of them come out in one
+// ascending run.  From the n_pos positive candidates (keys >= cut.thr): 1 for that case, 0 when
+// thr is the reference's threshold, -1 when positives below cut.thr may exist and the count has
+// to come from the exact path.
+__device__ __forceinline__ int sparse_fast_case(uint32_t thr, int n_pos, const SampleCut& cut) {
+  if (thr <= kZeroKey || n_pos != kTopK) return 0;
+  return cut.thr <= kZeroKey + 1u ? 1 : -1;
+}
+
+// Resolves n (kTopK <= n <= CAP) collected candidates (keys >= cut.thr) that hold the row's top
+// 2048; load(e, k, t) fetches candidate e (from LDS, or from the row's published list).  A
+// histogram of their digit cand_digit gives the threshold digit t1: candidates above it are
+// taken, its members are ranked exactly by (key desc, token asc) -- a handful by the choice of
+// the digit -- which also gives the threshold key; the taken tokens then go out in order
+// (emit_sorted).  More members than threads (heavy ties) select the threshold by radix passes
+// and emit by re-reading the row r.  Returns false, having written nothing, when the row's
+// positive keys must be counted exactly first (sparse_fast_case): the caller runs exact_row.
+template <bool kVec, int NT, int CAP, typename Load>
+__device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, const SampleCut& cut, const RowSrc& r, const PtRow& pt,
+                              int32_t* dst, Load load) {
+  constexpr int EPT = CAP / NT;
+  static_assert(EPT * NT == CAP, "candidates split over the block");
+  static_assert(CAP >= 2 * kTopK && 3 * NT + kBins / 2 <= CAP, "LDS layout of the ordered emission");
+  const int tid = threadIdx.x;
+  uint32_t kk[EPT];
+  int tt[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {  // every load in flight before the first use
+    const int e = tid + j * NT;
+    kk[j] = 0u;
+    tt[j] = 0;
+    if (e < n) load(e, kk[j], tt[j]);
+  }
+  int32_t pv[EPT];  // page-table entries, fetched while the threshold is searched
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) pv[j] = tid + j * NT < n ? pt[tt[j]] : -1;
+  zero_lds<NT>(L.hist, kBins);
+  if (tid < 8) L.misc[tid] = 0;
+  __syncthreads();
+  int n_pos = 0;  // candidates with a positive key
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    if (tid + j * NT < n) {
+      atomicAdd(&L.hist[cand_digit(kk[j], cut)], 1);
+      n_pos += kk[j] > kZeroKey;
+    }
+  }
+  n_pos = wave_sum(n_pos);
+  if (lane_id() == 0 && n_pos) atomicAdd(&L.misc[4], n_pos);
+  __syncthreads();
+  find_threshold<kBins, NT>(L.hist, kTopK, L.wtot, L.res);
+  const uint32_t t1 = static_cast<uint32_t>(L.res[0]);
+  const int above1 = L.res[1];
+  const int n_t1 = L.res[2];
+  const int need1 = kTopK - above1;
+  static_assert(EPT <= 16, "masks hold 16 candidates");
+  uint32_t fa = 0, fm = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const bool in = tid + j * NT < n;
+    const uint32_t d = cand_digit(kk[j], cut);
+    fa |= static_cast<uint32_t>(in && d > t1) << j;
+    fm |= static_cast<uint32_t>(in && d == t1) << j;
+  }
+  if (n_t1 > NT) {  // block-uniform: heavy ties at the threshold digit
+    int pm = wave_slot_n(__popc(fm), &L.misc[1]);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      if ((fm >> j) & 1u) {
+        L.ck[pm] = kk[j];
+        L.ci[pm] = tt[j];
+        ++pm;
+      }
+    }
+    __syncthreads();
+    int remaining;
+    const uint32_t thr = select_lds(L, n_t1, -1, need1, remaining);
+    const int plus0 = sparse_fast_case(thr, L.misc[4], cut);
+    if (plus0 < 0) return false;
+    emit_row<kVec, NT>(r, plus0 ? kZeroKey : thr, plus0 ? 0 : remaining, pt, dst, L.scan);
+    return true;
+  }
+  // LDS of the ordered emission: the taken tokens and their entries in L.ck, the members of
+  // digit t1 and the word prefixes in L.ci, the bitmap in L.hist
+  int* sel = reinterpret_cast<int*>(L.ck);
+  int* sel_v = sel + kTopK;
+  uint32_t* mk = reinterpret_cast<uint32_t*>(L.ci);
+  int* mt = L.ci + NT;
+  int* mv = L.ci + 2 * NT;
+  uint16_t* pre = reinterpret_cast<uint16_t*>(L.ci + CAP - kBins / 2);
+  {
+    int pa = wave_slot_n(__popc(fa), &L.misc[0]);
+    int pm = wave_slot_n(__popc(fm), &L.misc[1]);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      if ((fa >> j) & 1u) {
+        sel[pa] = tt[j];
+        sel_v[pa] = pv[j];
+        ++pa;
+      }
+      if ((fm >> j) & 1u) {
+        mk[pm] = kk[j];
+        mt[pm] = tt[j];
+        mv[pm] = pv[j];
+        ++pm;
+      }
+    }
+  }
+  __syncthreads();
+  bool take = false;
+  uint32_t k = 0u;
+  int tok = 0, val = 0;
+  if (tid < n_t1) {
+    k = mk[tid];
+    tok = mt[tid];
+    val = mv[tid];
+    int rank = 0;
+    int j = 0;
+#pragma unroll 4
+    for (; j + 4 <= n_t1; j += 4) {  // 16-B LDS reads (mk and mt are 16-B aligned)
+      const uint4 kj = *reinterpret_cast<const uint4*>(mk + j);
+      const int4 tj = *reinterpret_cast<const int4*>(mt + j);
+      rank += (kj.x > k || (kj.x == k && tj.x < tok)) + (kj.y > k || (kj.y == k && tj.y < tok)) +
+              (kj.z > k || (kj.z == k && tj.z < tok)) + (kj.w > k || (kj.w == k && tj.w < tok));
+    }
+    for (; j < n_t1; ++j) rank += mk[j] > k || (mk[j] == k && mt[j] < tok);
+    take = rank < need1;
+    if (rank == need1 - 1) L.misc[2] = static_cast<int>(k);  // the threshold key
+  }
+  __syncthreads();
+  const uint32_t thr = static_cast<uint32_t>(L.misc[2]);
+  const int plus0 = sparse_fast_case(thr, L.misc[4], cut);
+  if (plus0 < 0) return false;  // block-uniform
+  const bool ga = take && (plus0 || k > thr);
+  const bool gt = take && !plus0 && k == thr;
+  const int sa = wave_slot(ga, &L.misc[0]);
+  const int st = kTopK - 1 - wave_slot(gt, &L.misc[3]);
+  if (ga) {
+    sel[sa] = tok;
+    sel_v[sa] = val;
+  }
+  if (gt) {
+    sel[st] = tok;
+    sel_v[st] = val;
+  }
+  __syncthreads();
+  emit_sorted<NT>(sel, L.misc[0], [&](int i) { return sel_v[i]; }, reinterpret_cast<uint32_t*>(L.hist), pre, L.wtot,
+                  r.len, dst);
+  return true;
+}
+
+// A row of at most kSample tokens: every key goes to the candidate list at its token's
+// position (no threshold, no collection pass) and is resolved on the plain 12-bit digit.
+template <bool kVec, int NT, int CAP>
+__device__ __forceinline__ bool small_row(ResolveLds<NT, CAP>& L, const RowSrc& r, const PtRow& pt, int32_t* dst) {
+  static_assert(CAP >= kSample, "the row fits the candidate list");
+  constexpr int QPT = kSample / 4 / NT;
+#pragma unroll
+  for (int j = 0; j < QPT; ++j) {
+    const int i0 = (static_cast<int>(threadIdx.x) + j * NT) * 4;
+    Quad q;
+    load_quad<kVec>(r, i0, q);
+    uint32_t k[4];
+    const uint32_t v = quad_keys(r, i0, q, k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if ((v >> e) & 1u) {
+        L.ck[i0 + e] = k[e];
+        L.ci[i0 + e] = i0 + e;
+      }
+    }
+  }
+  __syncthreads();
+  SampleCut cut;
+  cut.thr = 0u;
+  cut.shift = 20;
+  return resolve_cands<kVec>(L, r.len, cut, r, pt, dst, [&](int e, uint32_t& k, int& t) {
+    k = L.ck[e];
+    t = L.ci[e];
+  });
 }
 
 struct TopkArgs {
@@ -990,48 +1040,12 @@ __device__ __forceinline__ void copy_short_row(const PtRow& pt, int32_t* dst, in
   for (int i = threadIdx.x; i < kTopK; i += NT) dst[i] = i < len ? pt[i] : -1;
 }
 
-// The exact two-pass selection of one row by one CTA: pass-1 histogram, collection above / in
-// the threshold bin (s_a: kTopK staged tokens above it; at most cap_c candidates in L.ck /
-// L.ci), resolution in LDS or by re-reading the row.  Not inlined: it is the rare path of the
-// sampled kernels, whose register budget it would otherwise set.
-template <bool kVec, int NT, int CAP>
-__device__ __attribute__((noinline)) void exact_row(ResolveLds<NT, CAP>& L, int* s_a, int cap_c, const RowSrc r,
-                                                    const PtRow pt, int32_t* dst) {
-  constexpr int kStep = NT * 4 * kUnroll;
-  int pos, zeros;
-  pass_hist<kVec, NT>(r, 0, r.len, L.hist, L.red, pos, zeros);
-  if (threadIdx.x == 0 && zeros) L.hist[kZeroBin] += zeros;
-  const int b0 = static_cast<int>(threadIdx.x) * 4;
-  Batch x0, x1;
-  load_batch<kVec, NT>(r, b0, x0);
-  load_batch<kVec, NT>(r, b0 + kStep, x1);
-  __syncthreads();
-  const Meta m = row_meta<NT>(L.hist, pos, zeros, L.wtot, L.res);
-  if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
-  __syncthreads();
-  Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, cap_c};
-  collect<kVec, NT>(r, b0, (r.len + kStep - 1) / kStep, m, st, x0, x1);
-  __syncthreads();
-  const int n_a = min(L.misc[0], kTopK);
-  const int n_c = L.misc[1];
-  for (int i = threadIdx.x; i < n_a; i += NT) put(dst, i, pt[s_a[i]]);
-  if (m.fast) {
-    ordered_scan<kVec, NT>(
-        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
-  } else if (n_c <= cap_c) {
-    resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
-  } else {
-    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
 // One CTA per row with pass 1 (histogram + counts) from a.ghist / a.gcnt (the logits kernel's
-// fused pass 1): the row is collected against its exact threshold bin.
+// fused pass 1): the row's threshold from its exact threshold bin, then the ordered emission.
 template <bool kVec>
 __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   __shared__ ResolveLds<kTk, kCapC> L;
-  __shared__ int s_a[kTopK];
   constexpr int kStep = kTk * 4 * kUnroll;
   const int row = blockIdx.x;
   const int len = row_len(a, row);
@@ -1043,43 +1057,30 @@ __global__ __launch_bounds__(kTk) void topk_single_kernel(const TopkArgs a) {
   }
   const RowSrc r = row_src(a, row, len);
   const int b0 = static_cast<int>(threadIdx.x) * 4;
-  const int n_batches = (len + kStep - 1) / kStep;
-  Batch x0, x1;
   // pass-1 slots (4 bins per thread) first, then the first two batches, so that waiting for
   // the histogram does not wait for the batches
   const int4 h4 = reinterpret_cast<const int4*>(a.ghist + static_cast<int64_t>(row) * kBins)[threadIdx.x];
   const int pos = a.gcnt[2 * row];
   const int zeros = a.gcnt[2 * row + 1];
+  if (pos <= kTopK && pos + zeros >= kTopK) {  // block-uniform: the threshold is +0
+    emit_row<kVec, kTk>(r, kZeroKey, kTopK - pos, pt, dst, L.scan);
+    return;
+  }
+  Batch x0, x1;
   load_batch<kVec, kTk>(r, b0, x0);
   load_batch<kVec, kTk>(r, b0 + kStep, x1);
-  Meta m;
-  m.pos = pos;
-  m.fast = pos <= kTopK && pos + zeros >= kTopK;
-  m.t1 = 0;
-  m.above1 = pos;
-  if (threadIdx.x == 0) L.misc[0] = L.misc[1] = 0;
-  if (!m.fast) {
-    const int h[4] = {h4.x, h4.y, h4.z, h4.w};
-    find_threshold_regs<kTk, 4>(h, kTopK, L.wtot, L.res);
-    m.t1 = static_cast<uint32_t>(L.res[0]);
-    m.above1 = L.res[1];
-  } else {
-    __syncthreads();
-  }
-  Stage st{s_a, L.ck, L.ci, &L.misc[0], &L.misc[1], kTopK, kCapC};
-  collect<kVec, kTk>(r, b0, n_batches, m, st, x0, x1);
+  if (threadIdx.x == 0) L.misc[1] = 0;
+  const int h[4] = {h4.x, h4.y, h4.z, h4.w};
+  find_threshold_regs<kTk, 4>(h, kTopK, L.wtot, L.res);
+  const uint32_t t1 = static_cast<uint32_t>(L.res[0]);
+  const int need1 = kTopK - L.res[1];
+  collect_bin<kVec, kTk>(r, b0, (len + kStep - 1) / kStep, t1, L.ck, L.ci, &L.misc[1], kCapC, x0, x1);
   __syncthreads();
-  const int n_a = min(L.misc[0], kTopK);
   const int n_c = L.misc[1];
-  for (int i = threadIdx.x; i < n_a; i += kTk) put(dst, i, pt[s_a[i]]);
-  if (m.fast) {
-    ordered_scan<kVec, kTk>(
-        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.scan);
-  } else if (n_c <= kCapC) {
-    resolve_lds(L, n_c, m.t1, m.above1, pt, dst);
-  } else {
-    resolve_rescan<kVec>(L, r, m.t1, m.above1, pt, dst);
-  }
+  int remaining;
+  const uint32_t thr = n_c <= kCapC ? select_lds(L, n_c, static_cast<int>(t1), need1, remaining)
+                                    : select_rescan<kVec>(L, r, t1, need1, remaining);
+  emit_row<kVec, kTk>(r, thr, remaining, pt, dst, L.scan);
 }
 
 // One 512-thread CTA per row against the sampled threshold K* (one read of the row), with the
@@ -1089,7 +1090,6 @@ template <bool kVec>
 __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void topk_row_sampled_kernel(
     const TopkArgs a) {
   __shared__ ResolveLds<kTs, kCapS> L;
-  __shared__ int s_a[kTopK];
   constexpr int kStep = kTs * 4 * kUnroll;
   const int row = blockIdx.x;
   const int len = row_len(a, row);
@@ -1100,31 +1100,31 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
     return;
   }
   const RowSrc r = row_src(a, row, len);
+  bool done = false;
   if (len <= kSample) {  // block-uniform
-    small_row<kVec, kTs>(L, r, pt, dst);
-    return;
-  }
-  const int b0 = static_cast<int>(threadIdx.x) * 4;
-  SampleLoads<kTs> smp;
-  sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
-  Batch x0, x1;
-  load_batch<kVec, kTs>(r, b0, x0);
-  load_batch<kVec, kTs>(r, b0 + kStep, x1);
-  const SampleLds S{L.hist, L.wtot, L.res};
-  const SampleCut cut = sample_threshold<kTs>(r, smp, S);
-  if (threadIdx.x == 0) L.misc[2] = 0;
-  __syncthreads();
-  collect_ge<kVec, kTs>(r, b0, (len + kStep - 1) / kStep, cut.thr, L.ck, L.ci, &L.misc[2], kCapS, x0, x1);
-  __syncthreads();
-  const int n = L.misc[2];
-  if (n >= kTopK && n <= kCapS) {  // block-uniform
-    resolve_cands(L, n, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
-      k = L.ck[e];
-      t = L.ci[e];
-    });
+    done = small_row<kVec, kTs>(L, r, pt, dst);
   } else {
-    exact_row<kVec, kTs>(L, s_a, kCapS, r, pt, dst);
+    const int b0 = static_cast<int>(threadIdx.x) * 4;
+    SampleLoads<kTs> smp;
+    sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
+    Batch x0, x1;
+    load_batch<kVec, kTs>(r, b0, x0);
+    load_batch<kVec, kTs>(r, b0 + kStep, x1);
+    const SampleLds S{L.hist, L.wtot, L.res};
+    const SampleCut cut = sample_threshold<kTs>(r, smp, S);
+    if (threadIdx.x == 0) L.misc[2] = 0;
+    __syncthreads();
+    collect_ge<kVec, kTs>(r, b0, (len + kStep - 1) / kStep, cut.thr, L.ck, L.ci, &L.misc[2], kCapS, x0, x1);
+    __syncthreads();
+    const int n = L.misc[2];
+    if (n >= kTopK && n <= kCapS) {  // block-uniform
+      done = resolve_cands<kVec>(L, n, cut, r, pt, dst, [&](int e, uint32_t& k, int& t) {
+        k = L.ck[e];
+        t = L.ci[e];
+      });
+    }
   }
+  if (!done) exact_row<kVec, kTs>(L, r, pt, dst);  // block-uniform
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1138,10 +1138,9 @@ __global__ __launch_bounds__(256) void topk_zero_kernel(int32_t* __restrict__ ct
 struct SplitLds {
   union {
     struct {
-      int a[kTopK];
       uint32_t ck[kCapS];
       int ci[kCapS];
-    } col;                          // collection staging of this CTA's slice
+    } col;                          // this CTA's candidates of the threshold bin
     ResolveLds<kTs, kCapS> res;     // the row's resolution (last CTA only)
   } u;
   int wtot[kTs / kWave];
@@ -1170,7 +1169,7 @@ struct SampledLds {
 // that every CTA streams about L / T tokens whatever the length mix; the sum is <= T + rows, the
 // grid.  Needs rows <= kTs.  s_slot = {row (-1: none), index among the row's CTAs, c_r}.
 template <typename Lds>
-__device__ void split_assign(const TopkArgs& a, int T, Lds& L) {
+__device__ __forceinline__ void split_assign(const TopkArgs& a, int T, Lds& L) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
@@ -1247,73 +1246,72 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
     if (slice == 0) copy_short_row<kTs>(pt_row(a, row), a.out + static_cast<int64_t>(row) * kTopK, len);
     return;
   }
-  if (len <= kSample) {  // the whole row in one CTA, no split
-    if (slice == 0) small_row<kVec, kTs>(L.u.res, row_src(a, row, len), pt_row(a, row),
-                                         a.out + static_cast<int64_t>(row) * kTopK);
-    return;
-  }
-  int begin, end, n_sl;
-  if (!split_slice(len, a.S, slice, begin, end, n_sl)) return;
-
   const RowSrc r = row_src(a, row, len);
-  const RowSrc rr = row_src(a, row, end);
-  const int b0 = begin + tid * 4;
-  SampleLoads<kTs> smp;
-  sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
-  Batch x0, x1;
-  load_batch<kVec, kTs>(rr, b0, x0);
-  load_batch<kVec, kTs>(rr, b0 + kStep, x1);
-  if (tid == 0) L.n[0] = 0;
-  const SampleLds S{L.u.res.hist, L.wtot, L.res};
-  const SampleCut cut = sample_threshold<kTs>(r, smp, S);
-  collect_ge<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, cut.thr, L.u.col.ck, L.u.col.ci, &L.n[0], kCapS, x0,
-                        x1);
-  __syncthreads();
+  // the output row and page-table row are formed where they are used, so that nothing beyond
+  // the row's scores stays live across the collection loop
+  auto dst = [&]() { return a.out + static_cast<int64_t>(row) * kTopK; };
+  bool done = false;
+  if (len <= kSample) {  // the whole row in one CTA, no split
+    if (slice != 0) return;
+    done = small_row<kVec, kTs>(L.u.res, r, pt_row(a, row), dst());
+  } else {
+    int begin, end, n_sl;
+    if (!split_slice(len, a.S, slice, begin, end, n_sl)) return;
+    const RowSrc rr = row_src(a, row, end);
+    const int b0 = begin + tid * 4;
+    SampleLoads<kTs> smp;
+    sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
+    Batch x0, x1;
+    load_batch<kVec, kTs>(rr, b0, x0);
+    load_batch<kVec, kTs>(rr, b0 + kStep, x1);
+    if (tid == 0) L.n[0] = 0;
+    const SampleLds S{L.u.res.hist, L.wtot, L.res};
+    const SampleCut cut = sample_threshold<kTs>(r, smp, S);
+    collect_ge<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, cut.thr, L.u.col.ck, L.u.col.ci, &L.n[0], kCapS,
+                          x0, x1);
+    __syncthreads();
 
-  const int n_loc = L.n[0];
-  int32_t* ctr = a.ctr + static_cast<int64_t>(row) * a.ctr_stride;
-  // words 0..1 of the row's counters as one 64-bit word: low = keys published, high = CTAs done
-  unsigned long long* const pub = reinterpret_cast<unsigned long long*>(ctr);
-  if (tid == 0) L.n[1] = n_loc ? static_cast<int>(atomicAdd(pub, static_cast<unsigned long long>(n_loc))) : 0;
-  __syncthreads();
-  uint32_t* lk = a.c_keys + static_cast<int64_t>(row) * kCapS;
-  int32_t* lt = a.c_tok + static_cast<int64_t>(row) * kCapS;
-  const int base = L.n[1];
-  const int n_put = min(n_loc, kCapS);
-  for (int i = tid; i < n_put; i += kTs) {
-    const int j = base + i;
-    if (j < kCapS) {
-      __hip_atomic_store(&lk[j], L.u.col.ck[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&lt[j], L.u.col.ci[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int n_loc = L.n[0];
+    int32_t* ctr = a.ctr + static_cast<int64_t>(row) * a.ctr_stride;
+    // words 0..1 of the row's counters as one 64-bit word: low = keys published, high = CTAs done
+    unsigned long long* const pub = reinterpret_cast<unsigned long long*>(ctr);
+    if (tid == 0) L.n[1] = n_loc ? static_cast<int>(atomicAdd(pub, static_cast<unsigned long long>(n_loc))) : 0;
+    __syncthreads();
+    uint32_t* lk = a.c_keys + static_cast<int64_t>(row) * kCapS;
+    int32_t* lt = a.c_tok + static_cast<int64_t>(row) * kCapS;
+    const int base = L.n[1];
+    const int n_put = min(n_loc, kCapS);
+    for (int i = tid; i < n_put; i += kTs) {
+      const int j = base + i;
+      if (j < kCapS) {
+        __hip_atomic_store(&lk[j], L.u.col.ck[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&lt[j], L.u.col.ci[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // Every wave's stores complete before the barrier, so the row's done count below comes after
+    // them; the CTA that completes the count reads them back with device-coherent loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      // every CTA adds its count before its done mark, so the last mark returns the final count
+      const unsigned long long old = atomicAdd(pub, 1ull << 32);
+      const bool last = static_cast<int>(old >> 32) == n_sl - 1;
+      L.n[2] = last;
+      L.n[3] = last ? static_cast<int>(old & 0xFFFFFFFFull) : 0;
+    }
+    __syncthreads();
+    if (!L.n[2]) return;
+
+    const int n_tot = L.n[3];
+    if (n_tot >= kTopK && n_tot <= kCapS) {  // block-uniform
+      done = resolve_cands<kVec>(L.u.res, n_tot, cut, r, pt_row(a, row), dst(), [&](int e, uint32_t& k, int& t) {
+        k = __hip_atomic_load(&lk[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        t = __hip_atomic_load(&lt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      });
     }
   }
-  // Every wave's stores complete before the barrier, so the row's done count below comes after
-  // them; the CTA that completes the count reads them back with device-coherent loads.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    // every CTA adds its count before its done mark, so the last mark returns the final count
-    const unsigned long long old = atomicAdd(pub, 1ull << 32);
-    const bool last = static_cast<int>(old >> 32) == n_sl - 1;
-    L.n[2] = last;
-    L.n[3] = last ? static_cast<int>(old & 0xFFFFFFFFull) : 0;
-  }
-  __syncthreads();
-  if (!L.n[2]) return;
-
-  const int n_tot = L.n[3];
-  const PtRow pt = pt_row(a, row);
-  int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
-  if (n_tot >= kTopK && n_tot <= kCapS) {  // block-uniform
-    resolve_cands(L.u.res, n_tot, cut, pt, dst, [&](int e, uint32_t& k, int& t) {
-      k = __hip_atomic_load(&lk[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      t = __hip_atomic_load(&lt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    });
-  } else {
-    // the estimate missed: the exact path over the row, its tokens above the threshold bin
-    // staged in the upper half of the token list and at most kCapS / 2 candidates below
-    exact_row<kVec, kTs>(L.u.res, L.u.res.ci + kCapS / 2, kCapS / 2, r, pt, dst);
-  }
+  // the estimate missed, or the positives must be counted: the exact path over the row
+  if (!done) exact_row<kVec, kTs>(L.u.res, r, pt_row(a, row), dst());  // block-uniform
 }
 
 template <bool kVec>
@@ -1344,44 +1342,32 @@ __global__ __launch_bounds__(kTs) void topk_split_kernel(const TopkArgs a) {
   load_batch<kVec, kTs>(rr, b0, x0);
   load_batch<kVec, kTs>(rr, b0 + kStep, x1);
 
-  Meta m;
-  m.pos = pos;
-  m.fast = pos <= kTopK && pos + zeros >= kTopK;
-  m.t1 = 0;
-  m.above1 = pos;
-  int cnt_t1 = 0;
-  if (tid == 0) L.n[0] = L.n[1] = 0;
-  if (!m.fast) {
+  const bool fast = pos <= kTopK && pos + zeros >= kTopK;
+  uint32_t t1 = 0;
+  int need1 = kTopK - pos, cnt_t1 = 0;
+  if (tid == 0) L.n[1] = 0;
+  if (!fast) {
     const int h[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
     find_threshold_regs<kTs, 8>(h, kTopK, L.wtot, L.res);
-    m.t1 = static_cast<uint32_t>(L.res[0]);
-    m.above1 = L.res[1];
+    t1 = static_cast<uint32_t>(L.res[0]);
+    need1 = kTopK - L.res[1];
     cnt_t1 = L.res[2];
   } else {
     __syncthreads();
   }
-  // every CTA of the row takes the same decision: candidates are published only if the whole
-  // bin t1 of the row fits the resolver's LDS
-  const bool publish = !m.fast && cnt_t1 <= kCapS;
-  Stage st{L.u.col.a, L.u.col.ck, L.u.col.ci, &L.n[0], &L.n[1], kTopK, publish ? kCapS : 0};
-  collect<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, m, st, x0, x1);
-  __syncthreads();
-
-  const int n_a = min(L.n[0], kTopK);
-  const int n_c = min(L.n[1], kCapS);
+  // every CTA of the row takes the same decision: the threshold bin's candidates are collected
+  // and published only if the whole bin t1 of the row fits the resolver's LDS
+  const bool publish = !fast && cnt_t1 <= kCapS;
   int32_t* ctr = a.ctr + static_cast<int64_t>(row) * a.ctr_stride;
-  if (tid == 0) {
-    L.n[2] = n_a ? atomicAdd(&ctr[0], n_a) : 0;
-    L.n[3] = publish && n_c ? atomicAdd(&ctr[1], n_c) : 0;
-  }
-  __syncthreads();
-  const PtRow pt = pt_row(a, row);
-  int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
-  const int base_a = L.n[2];
-  for (int i = tid; i < n_a; i += kTs) put(dst, base_a + i, pt[L.u.col.a[i]]);
   uint32_t* lk = a.c_keys + static_cast<int64_t>(row) * kCapS;
   int32_t* lt = a.c_tok + static_cast<int64_t>(row) * kCapS;
-  if (publish) {
+  if (publish) {  // block-uniform
+    collect_bin<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, t1, L.u.col.ck, L.u.col.ci, &L.n[1], kCapS, x0,
+                           x1);
+    __syncthreads();
+    const int n_c = min(L.n[1], kCapS);
+    if (tid == 0) L.n[3] = n_c ? atomicAdd(&ctr[1], n_c) : 0;
+    __syncthreads();
     const int base_c = L.n[3];
     for (int i = tid; i < n_c; i += kTs) {
       const int j = base_c + i;
@@ -1402,23 +1388,24 @@ __global__ __launch_bounds__(kTs) void topk_split_kernel(const TopkArgs a) {
   __syncthreads();
   if (!L.n[4]) return;
 
+  // the last CTA of the row: the threshold, then the ordered emission over the whole row
   const RowSrc r = row_src(a, row, len);
-  if (m.fast) {
-    ordered_scan<kVec, kTs>(
-        r, [](uint32_t) { return true; }, kZeroKey, false, 0, m.pos, kTopK - m.pos, pt, dst, L.u.res.scan);
-    return;
+  const PtRow pt = pt_row(a, row);
+  int32_t* dst = a.out + static_cast<int64_t>(row) * kTopK;
+  uint32_t thr = kZeroKey;
+  int remaining = need1;
+  if (publish) {
+    const int n_tot = cnt_t1;  // every CTA published its share of bin t1 (cnt_t1 <= kCapS)
+    for (int i = tid; i < n_tot; i += kTs) {
+      L.u.res.ck[i] = __hip_atomic_load(&lk[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      L.u.res.ci[i] = __hip_atomic_load(&lt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    thr = select_lds(L.u.res, n_tot, static_cast<int>(t1), need1, remaining);
+  } else if (!fast) {
+    thr = select_rescan<kVec>(L.u.res, r, t1, need1, remaining);
   }
-  if (!publish) {
-    resolve_rescan<kVec>(L.u.res, r, m.t1, m.above1, pt, dst);
-    return;
-  }
-  const int n_tot = cnt_t1;  // every CTA published its share of bin t1 (cnt_t1 <= kCapS)
-  for (int i = tid; i < n_tot; i += kTs) {
-    L.u.res.ck[i] = __hip_atomic_load(&lk[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    L.u.res.ci[i] = __hip_atomic_load(&lt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  resolve_lds(L.u.res, n_tot, m.t1, m.above1, pt, dst);
+  emit_row<kVec, kTs>(r, thr, remaining, pt, dst, L.u.res.scan);
 }
 
 // Slices per row of the split path (1: one CTA per row).  At most ~3 split CTAs fit a CU.

@@ -6,13 +6,14 @@ rows).
 Decode (decode_1x4k, decode_32x16k, decode_mtp64 -- the headline): quant_q_fp8 -> mqa_logits(
 hist_lens=lens) -> sparse_mask_topk_transform on every row: q8 and the folded weights bit-exact,
 the nonzero mask bit-exact, every logit within the tolerance of tests/gpu_util.py against the
-exact fp64 oracle, every top-k row equal to the oracle's C radix select on the same logits.
+exact fp64 oracle, every top-k row identical (set and order) to the oracle's C radix select
+on the same logits.
 
 Prefill (prefill_8k_64k, prefill_16k_128k with Student-t K): quant_q_fp8 -> prefill_indexer in
-4096-row slabs.  Every row of every slab: the top-k set equals an exact selection computed by
-torch on the GPU from the same logits (int64 composite keys (key << 21) | (2^21 - 1 - token),
-i.e. key descending, token ascending).  About 32 rows spread over the slabs (the first and last
-row of each slab among them): q8 / weights bit-exact, logits against the fp64 oracle, and the
+4096-row slabs.  Every row of every slab equals an exact selection computed by torch on the GPU
+from the same logits (int64 composite keys (key << 21) | (2^21 - 1 - token), i.e. key
+descending, token ascending), put in the reference's order.  About 32 rows spread over the
+slabs (the first and last row of each slab among them): q8 / weights bit-exact, logits against the fp64 oracle, and the
 top-k row equal to the oracle's C radix select."""
 import numpy as np
 import pytest
@@ -63,15 +64,17 @@ def test_decode_config_full_size(gpu, name):
         worst = max(worst, wm)
     want = topk_radix(got, got_mask, case.context_lens.numpy(), pt.numpy(), case.width)
     sel = out.cpu().numpy()
-    bad = [r for r in range(case.rows) if not np.array_equal(np.sort(sel[r]), np.sort(want[r]))]
+    bad = [r for r in range(case.rows) if not np.array_equal(sel[r], want[r])]
     assert not bad, f"{name}: top-k rows {bad[:8]} differ from the oracle's selection"
     _log(f"{name}: {case.rows} rows match; worst logit error / magnitude {worst:.2e}")
 
 
 def _exact_topk_torch(lg, lens, pt):
-    """int32 [rows, 2048]: page_table entries of each row's top-2048 tokens (key descending,
-    token ascending; -1 padded below 2048 tokens), sorted per row -- computed with torch on the
-    GPU from the logits lg [rows, width] (every entry below the row length valid)."""
+    """int32 [rows, 2048]: each row's top-2048 in the reference's output order -- the tokens with
+    key > thr ascending, then the ties taken ascending (-1 padded below 2048 tokens) -- as page_table
+    entries, computed with torch on the GPU from the logits lg [rows, width] (every entry below
+    the row length valid).  The selection is a top-k of int64 composite keys
+    (key << 21) | (2^21 - 1 - token): key descending, token ascending."""
     rows, width = lg.shape
     assert width < (1 << 21)
     b = lg.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
@@ -79,16 +82,29 @@ def _exact_topk_torch(lg, lens, pt):
     del b
     t = torch.arange(width, device=lg.device, dtype=torch.int64)
     comp = (key << 21) | ((1 << 21) - 1 - t)[None, :]
-    del key
     comp.masked_fill_(t[None, :] >= lens.long()[:, None], -1)
     k = min(2048, width)
     _, idx = torch.topk(comp, k, dim=1, sorted=False)
     del comp
-    sel = pt.long()[idx]
-    sel = torch.where(idx < lens.long()[:, None], sel, torch.full_like(sel, -1))
+    idx = idx.sort(dim=1).values                       # ascending token
+    ksel = key.gather(1, idx)
+    valid = idx < lens.long()[:, None]
+    # the threshold: +0 when positives <= 2048 <= positives + zeros (the reference's sparse fast
+    # path), else the 2048th largest key; a short row is copied in order
+    inrow = t[None, :] < lens.long()[:, None]
+    pos = ((key > 0x80000000) & inrow).sum(dim=1, keepdim=True)
+    zeros = ((key == 0x80000000) & inrow).sum(dim=1, keepdim=True)
+    thr = torch.where(valid, ksel, torch.full_like(ksel, 1 << 40)).min(dim=1, keepdim=True).values
+    thr = torch.where((pos <= 2048) & (pos + zeros >= 2048), torch.full_like(thr, 0x80000000), thr)
+    tie = (ksel == thr) & valid & (lens.long()[:, None] > 2048)
+    order = torch.sort(tie.to(torch.int8) + 2 * (~valid).to(torch.int8), dim=1, stable=True).indices
+    idx = idx.gather(1, order)
+    valid = valid.gather(1, order)
+    del key, inrow
+    sel = torch.where(valid, pt.long()[idx], torch.full_like(idx, -1))
     out = torch.full((rows, 2048), -1, dtype=torch.int64, device=lg.device)
     out[:, :k] = sel
-    return out.to(torch.int32).sort(dim=1).values
+    return out.to(torch.int32)
 
 
 @pytest.mark.timeout(1200)
@@ -116,14 +132,13 @@ def test_prefill_config_full_size(gpu, name):
         r0, r1 = s * SLAB, min(rows, (s + 1) * SLAB)
         lg = hcu_ops.mqa_logits_prefill(q8[r0:r1], w[r0:r1], kv, bt, lens[r0:r1], width)
         want = _exact_topk_torch(lg, lens[r0:r1], ptg)
-        got = out[r0:r1].sort(dim=1).values
-        diff = (got != want).any(dim=1).nonzero().flatten()
-        assert diff.numel() == 0, f"{name}: slab {s} rows {(diff[:8] + r0).tolist()} differ from the exact set"
+        diff = (out[r0:r1] != want).any(dim=1).nonzero().flatten()
+        assert diff.numel() == 0, f"{name}: slab {s} rows {(diff[:8] + r0).tolist()} differ from the exact selection"
         for r in picks:
             if r0 <= r < r1:
                 kept[r] = lg[r - r0].cpu().numpy()
-        del lg, want, got
-        _log(f"{name}: slab {s} ({r1 - r0} rows) top-k sets exact")
+        del lg, want
+        _log(f"{name}: slab {s} ({r1 - r0} rows) top-k rows exact")
 
     idx = np.array(picks)
     rq8, rw = O.quant_q(q_bits(case.q[idx]), case.w[idx].numpy())
@@ -138,5 +153,5 @@ def test_prefill_config_full_size(gpu, name):
         wm, _ = check_logits(kept[r][:L], ref, mag, f"{name} row {r}")
         worst = max(worst, wm)
         want = topk_radix(kept[r][None, :], None, np.array([L], dtype=np.int32), pt.numpy()[None, :], width)
-        assert np.array_equal(np.sort(sel[i]), np.sort(want[0])), f"{name}: row {r} differs from the oracle"
+        assert np.array_equal(sel[i], want[0]), f"{name}: row {r} differs from the oracle"
     _log(f"{name}: {len(picks)} sampled rows match the oracle; worst logit error / magnitude {worst:.2e}")

@@ -1,7 +1,9 @@
-"""GPU parity of the exact top-2048 + page-table transform: the selected sets (rows compared
-sorted) equal the oracle's on the same scores, for the reference's ten score distributions
-(hcu_ops/tests/topk_lib.py:8-51), ragged / padded rows, the 1M-wide production layout, every
-split count, the fused pass-1 path and the varlen layout."""
+"""GPU parity of the exact top-2048 + page-table transform: every output row is identical to
+the oracle's C restatement of the reference single kernel (hcu_ops/csrc/sparse_mask_topk.cu:
+141-349) on the same scores -- the same set and the same order (keys above the threshold in
+ascending token order, then the ties taken in ascending token order) -- for the reference's ten
+score distributions (hcu_ops/tests/topk_lib.py:8-51), ragged / padded rows, the 1M-wide
+production layout, every split count, the fused pass-1 path and the varlen layout."""
 import numpy as np
 import pytest
 import torch
@@ -12,7 +14,6 @@ import workloads as wl
 from oracle import indexer as O
 from oracle.topk_c import topk_radix
 
-from gpu_util import sorted_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -37,11 +38,11 @@ def test_topk_distributions(gpu, dist, B):
         for ragged in [False, True]:
             W = 2 * L + 64 if ragged and L >= 16384 else L + 64
             x, mask, lengths, pt = wl.topk_scores(B, L, dist, W=W, ragged=ragged, seed=L + B)
-            ref = sorted_rows(_oracle(x, mask, lengths, pt, W))
+            ref = np.asarray(_oracle(x, mask, lengths, pt, W))
             xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
             cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
             for name, fn in IMPLS.items():
-                got = sorted_rows(fn(xg, mg, lg, pg, cu).cpu().numpy())
+                got = np.asarray(fn(xg, mg, lg, pg, cu).cpu().numpy())
                 assert np.array_equal(got, ref), f"{dist} B={B} L={L} ragged={ragged} impl={name}"
 
 
@@ -50,21 +51,21 @@ def test_topk_production_width(gpu, dist):
     """Score width = page-table capacity (1M) with ragged rows of 16K..128K tokens."""
     for L in [16384, 131072]:
         x, mask, lengths, pt = wl.topk_scores(6, L, dist, W=1 << 20, ragged=True, seed=L)
-        ref = sorted_rows(_oracle(x, mask, lengths, pt, 1 << 20))
+        ref = np.asarray(_oracle(x, mask, lengths, pt, 1 << 20))
         xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
         cu = torch.arange(7, dtype=torch.int32, device=gpu)
         for name, fn in IMPLS.items():
-            got = sorted_rows(fn(xg, mg, lg, pg, cu).cpu().numpy())
+            got = np.asarray(fn(xg, mg, lg, pg, cu).cpu().numpy())
             assert np.array_equal(got, ref), f"W1M {dist} L={L} impl={name}"
         del xg, mg, pg
 
 
 def test_topk_many_rows_and_empty(gpu):
     x, mask, lengths, pt = wl.topk_scores(600, 5000, "relu_sum", W=5056, ragged=True, seed=1)
-    ref = sorted_rows(_oracle(x, mask, lengths, pt, 5056))
+    ref = np.asarray(_oracle(x, mask, lengths, pt, 5056))
     out = hcu_ops.sparse_mask_topk_transform(x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu),
                                              torch.arange(601, dtype=torch.int32, device=gpu))
-    assert np.array_equal(sorted_rows(out.cpu().numpy()), ref)
+    assert np.array_equal(np.asarray(out.cpu().numpy()), ref)
     e = torch.empty(0, 4096, device=gpu)
     out = hcu_ops.sparse_mask_topk_transform(e, torch.empty(0, 256, dtype=torch.int16, device=gpu),
                                              torch.empty(0, dtype=torch.int32, device=gpu),
@@ -79,11 +80,11 @@ def test_topk_dense_and_varlen(gpu):
     lengths = torch.tensor([9000, 3000, 2048, 2049, 8999, 100, 6000], dtype=torch.int32)
     cu = torch.tensor([0, 3, 4, 7], dtype=torch.int32)
     pt = (torch.arange(9000, dtype=torch.int32)[None, :] + 100000 * torch.arange(3, dtype=torch.int32)[:, None])
-    ref = sorted_rows(_oracle(x, None, lengths, pt, 9000, cu=cu))
+    ref = np.asarray(_oracle(x, None, lengths, pt, 9000, cu=cu))
     for splits in [1, 4]:
         got = hcu_ops.topk_transform(x.to(gpu), lengths.to(gpu), pt.contiguous().to(gpu), cu.to(gpu),
                                      max_splits=splits)
-        assert np.array_equal(sorted_rows(got.cpu().numpy()), ref), f"splits={splits}"
+        assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"splits={splits}"
 
 
 @pytest.mark.parametrize("fused", [False, True])
@@ -107,8 +108,8 @@ def test_topk_pass1_pairing(gpu, monkeypatch, fused, group, lens):
     assert hcu_ops._MQA_HIST is None
     plain = _C.sparse_mask_topk_transform(lg, mask, lens, pt, cu, 2048)
     ref = _oracle(lg.cpu(), mask.cpu(), case.context_lens, case.page_table_1(), case.width)
-    assert np.array_equal(sorted_rows(paired.cpu().numpy()), sorted_rows(ref))
-    assert np.array_equal(sorted_rows(plain.cpu().numpy()), sorted_rows(ref))
+    assert np.array_equal(np.asarray(paired.cpu().numpy()), np.asarray(ref))
+    assert np.array_equal(np.asarray(plain.cpu().numpy()), np.asarray(ref))
 
 
 def _sample_tokens(L):
@@ -138,17 +139,17 @@ def test_topk_sampled_threshold_fallback(gpu, pattern):
             x[b, keep] += 10.0
     mask = torch.full((B, (W + 15) // 16), -1, dtype=torch.int16)
     pt = (torch.arange(W, dtype=torch.int32)[None, :] + 7 + 1000000 * torch.arange(B, dtype=torch.int32)[:, None])
-    ref = sorted_rows(_oracle(x, mask, lengths, pt, W))
+    ref = np.asarray(_oracle(x, mask, lengths, pt, W))
     xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
     cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
     for name, fn in IMPLS.items():
-        got = sorted_rows(fn(xg, mg, lg, pg, cu).cpu().numpy())
+        got = np.asarray(fn(xg, mg, lg, pg, cu).cpu().numpy())
         assert np.array_equal(got, ref), f"{pattern} impl={name}"
     got = hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1)
-    assert np.array_equal(sorted_rows(got.cpu().numpy()), ref), f"{pattern} dense"
+    assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"{pattern} dense"
     # into a caller's buffer: rows 1.. of a larger output, the other rows untouched
     buf = torch.full((B + 1, 2048), -7, dtype=torch.int32, device=gpu)
     ret = hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1, out=buf[1:])
     assert ret.data_ptr() == buf[1:].data_ptr()
-    assert np.array_equal(sorted_rows(buf[1:].cpu().numpy()), ref), f"{pattern} dense into out"
+    assert np.array_equal(np.asarray(buf[1:].cpu().numpy()), ref), f"{pattern} dense into out"
     assert (buf[0] == -7).all()

@@ -224,17 +224,33 @@ def test_topk_bruteforce_vs_c_radix(dist, L, ragged):
             assert tie_sel.max() < tie_uns.min()
 
 
-def test_topk_c_radix_output_order_is_reference_order():
-    """[keys > threshold, ascending t][ties, ascending t] (sparse_mask_topk.cu:301-348)."""
-    x, mask, lengths, pt = wl.topk_scores(2, 6000, "ties", seed=3)
-    out = topk_radix(x.numpy(), mask.numpy(), lengths.numpy(), pt.numpy(), 6000)
-    for r in range(2):
-        tok = out[r] - 7 - 1000000 * r
-        keys = O.row_keys(x.numpy()[r], mask.numpy()[r], 6000)[tok]
-        thr = keys.min()
-        n_above = int((keys > thr).sum())
-        assert np.all(np.diff(tok[:n_above]) > 0) and np.all(np.diff(tok[n_above:]) > 0)
-        assert np.all(keys[:n_above] > thr) and np.all(keys[n_above:] == thr)
+@pytest.mark.parametrize("dist", wl.TOPK_DISTS)
+def test_topk_c_radix_output_order_is_reference_order(dist):
+    """[keys > threshold, ascending t][ties, ascending t] (sparse_mask_topk.cu:301-348), the
+    threshold being +0 whenever positives <= 2048 <= positives + zeros (the sparse fast path,
+    :199-234; with exactly 2048 positives every selected key is above it) and the 2048th largest
+    key otherwise: the C restatement's rows equal the brute-force selection put in that order.
+    Rows with exactly 2048 positives (the smallest positive would otherwise count as a tie) are
+    included on purpose."""
+    x, mask, lengths, pt = wl.topk_scores(3, 6000, dist, W=6064, ragged=True, seed=3)
+    xs, ms, ls, ps = x.numpy(), mask.numpy(), lengths.numpy(), pt.numpy()
+    x2 = np.random.default_rng(5).standard_normal((2, 5000)).astype(np.float32)
+    x2[:, :2048] = np.abs(x2[:, :2048]) + 1e-3  # exactly 2048 positives
+    x2[:, 2048:] = -np.abs(x2[:, 2048:])
+    x2[1, 3000:3100] = 0.0                      # ... and some zeros
+    x2 = np.ascontiguousarray(np.stack([np.random.default_rng(6 + i).permutation(x2[i]) for i in range(2)]))
+    cases = [(xs, ms, ls, ps, 6064), (x2, None, np.array([5000, 5000], dtype=np.int32),
+                                      np.tile(np.arange(5000, dtype=np.int32), (2, 1)) + 11, 5000)]
+    for xs, ms, ls, ps, W in cases:
+        out = topk_radix(xs, ms, ls, ps, W)
+        for r in range(xs.shape[0]):
+            n = min(int(ls[r]), W)
+            keys = O.row_keys(xs[r], None if ms is None else ms[r], n)
+            sel = O.topk_tokens(keys)  # ascending t
+            pos, zeros = int((keys > O.ZERO_KEY).sum()), int((keys == O.ZERO_KEY).sum())
+            thr = O.ZERO_KEY if pos <= 2048 <= pos + zeros else keys[sel].min()
+            want = np.concatenate([sel[keys[sel] > thr], sel[keys[sel] == thr]])
+            assert np.array_equal(out[r], ps[r][want])
 
 
 def test_topk_pure_python_tiny():
