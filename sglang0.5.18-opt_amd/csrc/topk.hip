@@ -14,7 +14,7 @@
 // streaming loop); they are resolved exactly by a 12-bit histogram of a digit relative to K*
 // (sized from the sample so that the threshold digit holds a handful of keys) and an exact
 // (key desc, token asc) rank of that digit's members; the selected tokens are then put in order
-// by a bitmap of the row's tokens and a prefix count of its words (emit_sorted).  If the count
+// by a bitmap of the row's tokens and a prefix count of its words (emit_held).  If the count
 // misses [2048, capacity] the row takes the exact path, so the result never depends on the sample.
 // Exact path (radix digits 12/12/8 of the 32-bit key):
 //   pass 1   histogram of key[31:20] over the nonzero tokens plus positive / zero counts (or
@@ -708,33 +708,38 @@ __device__ __forceinline__ void emit_row(const RowSrc& r, uint32_t thr, int rema
   }
 }
 
-// Ordered emission of a resolved selection held in an LDS list: sel[0, nA) the tokens with key >
-// thr, sel[kTopK - nT, kTopK) the ties taken (nA + nT == kTopK), each part in any order, val(i)
-// the page-table entry of sel[i].  Per window of kEmitWin tokens, a bitmap of each part's tokens
-// (`bits`, 4096 words: [0, 2048) the first part, [2048, 4096) the ties) and the prefix counts of
-// its words (`pre`) give every token its rank within its part, its slot dst[rank] (first part)
-// or dst[nA + rank] (ties).  Four barriers a window; one window covers a row of up to 64K tokens.
+// Ordered emission of a resolved selection whose tokens the block's threads hold in registers:
+// each(fn) calls fn(token, tie, value) for every taken token this thread holds (tie: key == the
+// threshold, else key above it; value: its page-table entry).  Per window of kEmitWin tokens, a
+// bitmap of each part's tokens (`bits`, 4096 words: [0, 2048) above the threshold, [2048, 4096)
+// the ties) and the prefix counts of its words (`pre`) give every token its rank within its
+// part: slot rank for the first part, n_above + rank for the ties (the reference's order).
+// Window 0's bitmap must be zero on entry; *n_ties is read after the first barrier.  Three
+// barriers a window; one window covers a row of up to 64K tokens.
 constexpr int kEmitWords = kBins / 2;
 constexpr int kEmitWin = kEmitWords * 32;
 
-template <int NT, typename Val>
-__device__ __forceinline__ void emit_sorted(const int* sel, int nA, Val val, uint32_t* bits, uint16_t* pre, int* s_w, int len,
-                            int32_t* dst) {
+template <int NT, typename Each>
+__device__ __forceinline__ void emit_held(Each each, const int* n_ties, uint32_t* bits, uint16_t* pre, int* s_w,
+                                          int len, int32_t* dst) {
   constexpr int WPT = kBins / NT;  // words a thread zeroes and counts; all of one part
   static_assert(WPT * NT == kBins && WPT % 4 == 0 && kEmitWords % WPT == 0, "bitmap split over the block");
   const int tid = threadIdx.x;
-  int base_a = 0, base_t = nA;
+  uint4* b4 = reinterpret_cast<uint4*>(bits + tid * WPT);
+  int base_a = 0, base_t = 0;
   for (int w0 = 0; w0 < len; w0 += kEmitWin) {  // block-uniform
-    uint4* b4 = reinterpret_cast<uint4*>(bits + tid * WPT);
+    if (w0 > 0) {
 #pragma unroll
-    for (int j = 0; j < WPT / 4; ++j) b4[j] = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
-    for (int i = tid; i < kTopK; i += NT) {
-      const int x = sel[i] - w0;
-      if (static_cast<unsigned>(x) < static_cast<unsigned>(kEmitWin))
-        atomicOr(&bits[(i < nA ? 0 : kEmitWords) + (x >> 5)], 1u << (x & 31));
+      for (int j = 0; j < WPT / 4; ++j) b4[j] = make_uint4(0u, 0u, 0u, 0u);
+      __syncthreads();
     }
+    each([&](int tok, bool tie, int32_t) {
+      const int x = tok - w0;
+      if (static_cast<unsigned>(x) < static_cast<unsigned>(kEmitWin))
+        atomicOr(&bits[(tie ? kEmitWords : 0) + (x >> 5)], 1u << (x & 31));
+    });
     __syncthreads();
+    if (w0 == 0) base_t = kTopK - *n_ties;
     int pc[WPT];
     int c = 0;
 #pragma unroll
@@ -758,17 +763,17 @@ __device__ __forceinline__ void emit_sorted(const int* sel, int nA, Val val, uin
 #pragma unroll
     for (int j = 0; j < WPT; ++j) pre[tid * WPT + j] = static_cast<uint16_t>(ex + pc[j]);
     __syncthreads();
-    for (int i = tid; i < kTopK; i += NT) {
-      const int x = sel[i] - w0;
+    each([&](int tok, bool tie, int32_t v) {
+      const int x = tok - w0;
       if (static_cast<unsigned>(x) < static_cast<unsigned>(kEmitWin)) {
-        const int wd = (i < nA ? 0 : kEmitWords) + (x >> 5);
+        const int wd = (tie ? kEmitWords : 0) + (x >> 5);
         const int rank = pre[wd] + __popc(bits[wd] & ((1u << (x & 31)) - 1u));
-        put(dst, (i < nA ? base_a : base_t) + rank, val(i));
+        put(dst, (tie ? base_t : base_a) + rank, v);
       }
-    }
+    });
     base_a += tot_a;
     base_t += total - tot_a;
-    __syncthreads();
+    if (w0 + kEmitWin < len) __syncthreads();  // the next window reuses bits, pre and s_w
   }
 }
 
@@ -805,12 +810,14 @@ __device__ __forceinline__ void exact_row(ResolveLds<NT, CAP>& L, const RowSrc& 
 
 // The reference takes the threshold +0, with no ties, whenever positives <= 2048 <= positives +
 // zeros (its sparse fast path, sparse_mask_topk.cu:199-234); that differs from the 2048th largest
-// key thr only when the row holds exactly 2048 positive keys -- then all of them come out in one
-// ascending run.  From the n_pos positive candidates (keys >= cut.thr): 1 for that case, 0 when
-// thr is the reference's threshold, -1 when positives below cut.thr may exist and the count has
+// key only when the row holds exactly 2048 positive keys -- then all of them come out in one
+// ascending run.  The candidates hold every key >= cut.thr, so exactly 2048 positive candidates
+// are the whole selection; the row then has no other positive key if cut.thr <= the smallest
+// positive key.  From the n_pos positive candidates: 1 for that case, 0 when the 2048th largest
+// key is the reference's threshold, -1 when positives below cut.thr may exist and the count has
 // to come from the exact path.
-__device__ __forceinline__ int sparse_fast_case(uint32_t thr, int n_pos, const SampleCut& cut) {
-  if (thr <= kZeroKey || n_pos != kTopK) return 0;
+__device__ __forceinline__ int sparse_fast_case(int n_pos, const SampleCut& cut) {
+  if (n_pos != kTopK) return 0;
   return cut.thr <= kZeroKey + 1u ? 1 : -1;
 }
 
@@ -819,7 +826,7 @@ __device__ __forceinline__ int sparse_fast_case(uint32_t thr, int n_pos, const S
 // histogram of their digit cand_digit gives the threshold digit t1: candidates above it are
 // taken, its members are ranked exactly by (key desc, token asc) -- a handful by the choice of
 // the digit -- which also gives the threshold key; the taken tokens then go out in order
-// (emit_sorted).  More members than threads (heavy ties) select the threshold by radix passes
+// (emit_held).  More members than threads (heavy ties) select the threshold by radix passes
 // and emit by re-reading the row r.  Returns false, having written nothing, when the row's
 // positive keys must be counted exactly first (sparse_fast_case): the caller runs exact_row.
 template <bool kVec, int NT, int CAP, typename Load>
@@ -860,6 +867,8 @@ __device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, con
   const int above1 = L.res[1];
   const int n_t1 = L.res[2];
   const int need1 = kTopK - above1;
+  const int plus0 = sparse_fast_case(L.misc[4], cut);
+  if (plus0 < 0) return false;  // block-uniform
   static_assert(EPT <= 16, "masks hold 16 candidates");
   uint32_t fa = 0, fm = 0;
 #pragma unroll
@@ -882,29 +891,20 @@ __device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, con
     __syncthreads();
     int remaining;
     const uint32_t thr = select_lds(L, n_t1, -1, need1, remaining);
-    const int plus0 = sparse_fast_case(thr, L.misc[4], cut);
-    if (plus0 < 0) return false;
     emit_row<kVec, NT>(r, plus0 ? kZeroKey : thr, plus0 ? 0 : remaining, pt, dst, L.scan);
     return true;
   }
-  // LDS of the ordered emission: the taken tokens and their entries in L.ck, the members of
-  // digit t1 and the word prefixes in L.ci, the bitmap in L.hist
-  int* sel = reinterpret_cast<int*>(L.ck);
-  int* sel_v = sel + kTopK;
+  // The members of digit t1 go to L.ci, the bitmap of the ordered emission (zeroed here) is
+  // L.hist and its word prefixes the end of L.ci; the other taken tokens stay in registers.
   uint32_t* mk = reinterpret_cast<uint32_t*>(L.ci);
   int* mt = L.ci + NT;
   int* mv = L.ci + 2 * NT;
   uint16_t* pre = reinterpret_cast<uint16_t*>(L.ci + CAP - kBins / 2);
+  uint32_t* bits = reinterpret_cast<uint32_t*>(L.hist);
   {
-    int pa = wave_slot_n(__popc(fa), &L.misc[0]);
     int pm = wave_slot_n(__popc(fm), &L.misc[1]);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-      if ((fa >> j) & 1u) {
-        sel[pa] = tt[j];
-        sel_v[pa] = pv[j];
-        ++pa;
-      }
       if ((fm >> j) & 1u) {
         mk[pm] = kk[j];
         mt[pm] = tt[j];
@@ -912,16 +912,22 @@ __device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, con
         ++pm;
       }
     }
+    constexpr int WPT = kBins / NT;
+    uint4* b4 = reinterpret_cast<uint4*>(bits + tid * WPT);
+#pragma unroll
+    for (int j = 0; j < WPT / 4; ++j) b4[j] = make_uint4(0u, 0u, 0u, 0u);
   }
   __syncthreads();
-  bool take = false;
-  uint32_t k = 0u;
+  // A member is taken when its (key desc, token asc) rank is below need1; it is a tie when the
+  // members with a key >= its own reach need1, i.e. its key is the threshold (the need1-th).
+  // With exactly 2048 positive keys the reference's threshold is +0 and nothing is a tie.
+  bool take = false, tie = false;
   int tok = 0, val = 0;
   if (tid < n_t1) {
-    k = mk[tid];
+    const uint32_t k = mk[tid];
     tok = mt[tid];
     val = mv[tid];
-    int rank = 0;
+    int rank = 0, ge = 0;
     int j = 0;
 #pragma unroll 4
     for (; j + 4 <= n_t1; j += 4) {  // 16-B LDS reads (mk and mt are 16-B aligned)
@@ -929,30 +935,24 @@ __device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, con
       const int4 tj = *reinterpret_cast<const int4*>(mt + j);
       rank += (kj.x > k || (kj.x == k && tj.x < tok)) + (kj.y > k || (kj.y == k && tj.y < tok)) +
               (kj.z > k || (kj.z == k && tj.z < tok)) + (kj.w > k || (kj.w == k && tj.w < tok));
+      ge += (kj.x >= k) + (kj.y >= k) + (kj.z >= k) + (kj.w >= k);
     }
-    for (; j < n_t1; ++j) rank += mk[j] > k || (mk[j] == k && mt[j] < tok);
+    for (; j < n_t1; ++j) {
+      rank += mk[j] > k || (mk[j] == k && mt[j] < tok);
+      ge += mk[j] >= k;
+    }
     take = rank < need1;
-    if (rank == need1 - 1) L.misc[2] = static_cast<int>(k);  // the threshold key
+    tie = take && !plus0 && ge >= need1;
   }
-  __syncthreads();
-  const uint32_t thr = static_cast<uint32_t>(L.misc[2]);
-  const int plus0 = sparse_fast_case(thr, L.misc[4], cut);
-  if (plus0 < 0) return false;  // block-uniform
-  const bool ga = take && (plus0 || k > thr);
-  const bool gt = take && !plus0 && k == thr;
-  const int sa = wave_slot(ga, &L.misc[0]);
-  const int st = kTopK - 1 - wave_slot(gt, &L.misc[3]);
-  if (ga) {
-    sel[sa] = tok;
-    sel_v[sa] = val;
-  }
-  if (gt) {
-    sel[st] = tok;
-    sel_v[st] = val;
-  }
-  __syncthreads();
-  emit_sorted<NT>(sel, L.misc[0], [&](int i) { return sel_v[i]; }, reinterpret_cast<uint32_t*>(L.hist), pre, L.wtot,
-                  r.len, dst);
+  wave_slot(tie, &L.misc[3]);  // the tie count, read by emit_held after its first barrier
+  emit_held<NT>(
+      [&](auto&& fn) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+          if ((fa >> j) & 1u) fn(tt[j], false, pv[j]);
+        if (take) fn(tok, tie, val);
+      },
+      &L.misc[3], bits, pre, L.wtot, r.len, dst);
   return true;
 }
 
