@@ -67,13 +67,14 @@ def dequant_mla(cache, slots):
 
 
 # --------------------------------------------------------------------------------------------
-# Per-vector fp8 quantisation (hcu_ops/csrc/norm_quant.cu:13-14: amax = max|x|,
-# scale = amax / 448, q = fp8(x * (448 / amax)), amax == 0 -> 0), all in float32.
+# Per-vector fp8 quantisation (hcu_ops/csrc/norm_quant.cu:13-14: amax = max|x| taken with fmaxf
+# from 0, so NaN elements do not count, scale = amax / 448, q = fp8(x * (448 / amax)),
+# amax == 0 -> 0), all in float32.
 
 def quant_vectors(x):
     """x float32 [..., 128] -> (codes uint8 [..., 128], scale float32 [...])."""
     x = np.asarray(x, dtype=np.float32)
-    amax = np.max(np.abs(x), axis=-1)
+    amax = np.fmax.reduce(np.abs(x), axis=-1, initial=np.float32(0.0)).astype(np.float32)
     with np.errstate(divide="ignore"):
         inv = np.where(amax == 0, np.float32(0), np.float32(448.0) / amax).astype(np.float32)
     scale = (amax / np.float32(448.0)).astype(np.float32)

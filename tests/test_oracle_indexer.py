@@ -311,3 +311,41 @@ def test_cpu_baseline_row_matches_oracle():
                                   torch.from_numpy(slots.astype(np.int32)))
     # fp32 vs fp64 logits may reorder near-ties at the threshold: compare the sets up to a few
     assert len(set(got.tolist()) ^ set(ref[0].tolist())) <= 8
+
+
+def test_prefill_oracle_equals_decode_oracle_with_one_group():
+    """The prefill logits of one request's rows equal the decode logits of those rows as one
+    group sharing the request's block table (the same closed form, mqa_hist.cu:93-95,162): a
+    wrong causal rule, row offset or page mapping in either restatement breaks the equality."""
+    case = wl.prefill_case(31, 9, 700, heads=64)
+    q8, w = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
+    kv = _kv_np(case)
+    width = case.n_keys + 3
+    bt = np.concatenate([case.block_table.numpy(), np.zeros(1, dtype=np.int32)])
+    lens = case.lens.numpy().copy()
+    lens[2] = 0
+    lens[5] = width + 50  # clamped to the width by both
+    pre, pre_mag = O.mqa_logits_prefill(q8, w, kv, bt, lens, width)
+    bt2 = np.tile(bt, (case.rows, 1))
+    dec, dec_mag, _ = O.mqa_logits_decode(q8, w, kv, lens, bt2, case.rows, width)
+    assert np.array_equal(np.isnan(pre), np.isnan(dec))
+    assert np.array_equal(pre[~np.isnan(pre)], dec[~np.isnan(dec)]) and np.array_equal(pre_mag, dec_mag)
+    # and a causal row sees exactly its prefix: row i's logits are row j's on their common keys
+    L3, L4 = int(lens[3]), int(lens[4])
+    assert L3 < L4 and np.isnan(pre[3, L3:]).all() and not np.isnan(pre[4, :L4]).any()
+
+
+def test_quant_fmax_ignores_nan():
+    """amax follows fmaxf from 0 (hcu_ops/csrc/norm_quant.cu:13-14): NaN elements do not count;
+    an all-NaN vector has amax 0 (codes NaN, scale 0); inf gives scale inf and codes 0 / NaN."""
+    x = np.zeros((4, 128), dtype=np.float32)
+    x[0, :] = 1.0
+    x[0, 5] = np.nan
+    x[1, :] = np.nan
+    x[2, 3] = np.inf
+    x[2, 4] = 2.0
+    codes, scale = O.quant_vectors(x)
+    assert scale[0] == np.float32(1.0 / 448.0) and codes[0, 0] == 0x7E and codes[0, 5] in (0x7F, 0xFF)
+    assert scale[1] == 0 and (codes[1] & 0x7F == 0x7F).all()
+    assert np.isinf(scale[2]) and codes[2, 4] == 0 and codes[2, 3] & 0x7F == 0x7F
+    assert scale[3] == 0 and (codes[3] == 0).all()
