@@ -348,6 +348,105 @@ def kernel_time_ms(fn, torch, reps=20, rounds=5, settle_ms=50.0):
     return times[len(times) // 2]
 
 
+def cpu_threads(torch):
+    """The CPU baseline's threads: torch.set_num_threads(os.cpu_count()), as specified for the
+    baseline; the CPUs the process may run on are reported beside it."""
+    n = os.cpu_count() or 1
+    torch.set_num_threads(n)
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = n
+    return torch.get_num_threads(), avail
+
+
+def timed_steps(step, args, torch):
+    """ms per step: the step captured `steps_per_graph` to a hipGraph (as a serving loop captures the
+    indexer inside its model step), replayed untimed for settle_ms, then W warm-up steps, then
+    exactly K timed steps between two synchronisations (full graphs, then single-step graphs)."""
+    per = max(1, min(args.steps_per_graph, args.steps))
+    g = graph_of(step, torch, per)
+    g1 = graph_of(step, torch, 1) if args.steps % per or args.warmup % per else None
+    settle(g, torch, args.settle_ms)
+    for _ in range(args.warmup // per):
+        g.replay()
+    for _ in range(args.warmup % per):
+        g1.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps // per):
+        g.replay()
+    for _ in range(args.steps % per):
+        g1.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / args.steps, per
+
+
+def run_indexer(name, args, torch, dev, steps=None):
+    """One indexer workload: the timed step, its dominant kernel's roofline, the path roofline and
+    the CPU baseline, as the fields of a JSON line."""
+    import workloads as wl
+    t0 = time.perf_counter()
+    case = getattr(wl, name)()
+    log(f"built {name} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
+    decode = name.startswith("decode")
+    step = DecodeStep(case, dev) if decode else PrefillStep(case, dev)
+    torch.cuda.synchronize()
+    if steps is not None:
+        args = argparse.Namespace(**{**vars(args), **steps})
+    ms, per = timed_steps(step, args, torch)
+    tokens = step.tokens()
+    value = tokens / 1e3 / (ms / 1e3)
+    log(f"{name}: timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
+    if decode:
+        # the launch as the step makes it: logits + the paired top-k's workspace prepared
+        k_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
+        k0_ms = kernel_time_ms(step.logits_only, torch)
+        kb = step.logits_bytes()
+        achieved = kb / (k_ms / 1e3) / 1e9
+        traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", name)
+        roofline = {"bound": "hbm", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_bytes": kb,
+                    "kernel_us": round(k_ms * 1e3, 2), "without_topk_workspace_us": round(k0_ms * 1e3, 2)}
+        pb = step.path_bytes()
+        pa = pb / (ms / 1e3) / 1e9
+        path = {"bound": "hbm", "achieved": round(pa, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(pa / HBM_PEAK_GBS, 4), "algorithmic_bytes": pb}
+    else:
+        k_ms = kernel_time_ms(step.logits_only, torch)
+        kf = step.logits_flops()
+        achieved = kf / (k_ms / 1e3) / 1e12
+        # prefill runs the paged logits kernel with 8 query rows per CTA
+        traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", name)
+        roofline = {"bound": "mfma", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
+                    "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_flops": kf,
+                    "kernel_us": round(k_ms * 1e3, 2)}
+        pf = step.path_flops()
+        pa = pf / (ms / 1e3) / 1e12
+        path = {"bound": "mfma", "achieved": round(pa, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(pa / FP8_PEAK_TFLOPS, 4), "algorithmic_flops": pf}
+    log(f"{name}: logits kernel {k_ms * 1e3:.1f} us -> {roofline['achieved']} {roofline['unit']} "
+        f"({roofline['frac']:.1%})")
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads, avail = cpu_threads(torch)
+        v, sample = (decode_cpu_baseline if decode else prefill_cpu_baseline)(case, args.cpu_budget)
+        cpu = {"value": round(v, 2), "unit": "K-tokens/s", "cores": threads, "cpus_available": avail,
+               "kind": "port", "sample": sample, "cpu": cpu_model()}
+        log(f"{name}: cpu baseline {v:.4g} K-tokens/s on {threads} threads ({sample})")
+    config = {"workload": f"{name}: {WORKLOADS[name]}", "query_rows": int(case.rows),
+              "tokens_scored_per_step": int(tokens), "graph": f"hipGraph of {per} steps per replay",
+              "settle_ms": args.settle_ms}
+    return {"value": round(value, 1), "ms_per_step": round(ms, 5), "steps": args.steps, "warmup": args.warmup,
+            "config": config, "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -356,8 +455,10 @@ def main(argv=None):
     ap.add_argument("--settle-ms", type=float, default=200.0,
                     help="untimed replays of the step graph first, so that the GPU clocks have settled")
     ap.add_argument("--workload", default="decode_mtp64", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="the default decode_mtp64 line only (no prefill_8k_64k object)")
     ap.add_argument("--steps-per-graph", type=int, default=10, help="steps captured in one hipGraph")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB three times (the known-size kernel that "
@@ -381,92 +482,28 @@ def main(argv=None):
         torch.cuda.synchronize()
         log(f"copy calibration: 3 copies of {args.copy_calibration_mib} MiB")
         del src, dst
-    t0 = time.perf_counter()
-    case = getattr(wl, args.workload)()
-    log(f"built {args.workload} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
-    decode = args.workload.startswith("decode")
-    dequant = args.workload.startswith("dequant")
-    step = DecodeStep(case, dev) if decode else (DequantStep(case, dev) if dequant else PrefillStep(case, dev))
-    torch.cuda.synchronize()
-
-    # Steps are captured `steps_per_graph` to a hipGraph, as a serving loop captures the indexer
-    # inside its model step, so that one graph launch is not paid per tiny indexer step; the
-    # timed region runs exactly K steps (full graphs, then single-step graphs for the rest).
-    per = max(1, min(args.steps_per_graph, args.steps))
-    g = graph_of(step, torch, per)
-    g1 = graph_of(step, torch, 1) if args.steps % per or args.warmup % per else None
-    settle(g, torch, args.settle_ms)
-    for _ in range(args.warmup // per):
-        g.replay()
-    for _ in range(args.warmup % per):
-        g1.replay()
-    torch.cuda.synchronize()
-    log(f"warmup done ({args.settle_ms:.0f} ms of step replays, then {args.warmup} steps)")
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps // per):
-        g.replay()
-    for _ in range(args.steps % per):
-        g1.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    if dequant:
+    if args.workload.startswith("dequant"):
+        t0 = time.perf_counter()
+        case = getattr(wl, args.workload)()
+        log(f"built {args.workload} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
+        step = DequantStep(case, dev)
+        torch.cuda.synchronize()
+        ms, per = timed_steps(step, args, torch)
         return dequant_report(args, case, step, ms, per, torch)
-    tokens = step.tokens()
-    value = tokens / 1e3 / (ms / 1e3)
-    log(f"timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
 
-    if decode:
-        # the launch as the step makes it: logits + the paired top-k's counters zeroed
-        k_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
-        k0_ms = kernel_time_ms(step.logits_only, torch)
-        kb = step.logits_bytes()
-        achieved = kb / (k_ms / 1e3) / 1e9
-        traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", args.workload)
-        roofline = {"bound": "hbm", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_bytes": kb,
-                    "kernel_us": round(k_ms * 1e3, 2), "without_topk_workspace_us": round(k0_ms * 1e3, 2)}
-        pb = step.path_bytes()
-        pa = pb / (ms / 1e3) / 1e9
-        path = {"bound": "hbm", "achieved": round(pa, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(pa / HBM_PEAK_GBS, 4), "algorithmic_bytes": pb}
-    else:
-        k_ms = kernel_time_ms(step.logits_only, torch)
-        kf = step.logits_flops()
-        achieved = kf / (k_ms / 1e3) / 1e12
-        # prefill runs the paged logits kernel with 8 query rows per CTA
-        traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", args.workload)
-        roofline = {"bound": "mfma", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
-                    "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_flops": kf, "kernel_us": round(k_ms * 1e3, 2)}
-        pf = step.path_flops()
-        pa = pf / (ms / 1e3) / 1e12
-        path = {"bound": "mfma", "achieved": round(pa, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(pa / FP8_PEAK_TFLOPS, 4), "algorithmic_flops": pf}
-    log(f"logits kernel {k_ms * 1e3:.1f} us -> {roofline['achieved']} {roofline['unit']} ({roofline['frac']:.1%})")
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cores = torch.get_num_threads()
-        v, sample = (decode_cpu_baseline if decode else prefill_cpu_baseline)(case, args.cpu_budget)
-        cpu = {"value": round(v, 2), "unit": "K-tokens/s", "cores": cores, "kind": "port",
-               "sample": sample, "cpu": cpu_model()}
-        log(f"cpu baseline {v:.4g} K-tokens/s on {cores} threads ({sample})")
-
-    line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "K-tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)", "data": "synthetic (seeded, see tests/workloads.py)",
-        "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "query_rows": int(case.rows),
-                   "tokens_scored_per_step": int(tokens),
-                   "graph": f"hipGraph of {per} steps per replay",
-                   "settle_ms": args.settle_ms},
-        "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu,
-    }
+    head = run_indexer(args.workload, args, torch, dev)
+    line = {"metric": METRIC, "value": head["value"], "unit": "K-tokens/s", "n_gpus": 1, "steps": head["steps"],
+            "warmup": head["warmup"], "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)",
+            "data": "synthetic (seeded, see tests/workloads.py)", "config": head["config"],
+            "roofline": head["roofline"], "path_roofline": head["path_roofline"], "cpu_baseline": head["cpu_baseline"]}
+    if args.workload == "decode_mtp64" and not args.no_prefill:
+        # the second headline workload (the 64K-prefix chunked prefill) in the same line, its
+        # own step count sized to the same wall time
+        pre = run_indexer("prefill_8k_64k", args, torch, dev,
+                          steps={"steps": max(2, args.steps // 10), "warmup": max(1, args.warmup // 10),
+                                 "steps_per_graph": 1})
+        line["prefill_8k_64k"] = {"metric": METRIC, "unit": "K-tokens/s", **pre}
     print(json.dumps(line), flush=True)
     return 0
 
