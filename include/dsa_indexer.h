@@ -162,6 +162,22 @@ int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
                        const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
                        void* workspace, size_t workspace_bytes, int32_t* out, hipStream_t stream);
 
+/* dsa_topk_transform without the workspace argument, for callers that cannot allocate device
+ * memory (code under hipGraph capture with no allocator at hand, tight serving loops, harnesses
+ * that forbid allocation).  No counterpart in the reference.  The split path's workspace is a
+ * built-in device array of dsa_topk_noalloc_max_bytes() (8.0 MiB: up to 256 rows split) per device,
+ * held until the process ends; its address is looked up on the first call on each device.
+ * Inputs needing a larger workspace (dsa_topk_workspace_bytes) are rejected with
+ * DSA_ERR_WORKSPACE.  Every call on one device shares that device's array: calls that overlap on
+ * one device (concurrent streams or threads) race; the split counters are cleared on device at
+ * the start of every call.  Same results as dsa_topk_transform. */
+size_t dsa_topk_noalloc_max_bytes(void);
+int dsa_topk_transform_noalloc(const float* score, int64_t score_stride, int64_t width,
+                               const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
+                               int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
+                               const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                               int32_t* out, hipStream_t stream);
+
 /* dsa_topk_transform with pass 1 (histogram and counts) already built into hist_ws by
  * dsa_mqa_logits_decode(hist_lens = lengths) (replaces
  * _C.sparse_mask_topk_transform_split_pre, sparse_mask_topk.cu:986-1051).  hist_ws is the

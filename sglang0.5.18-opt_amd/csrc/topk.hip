@@ -30,6 +30,8 @@
 // global counters; the last CTA of the row to finish (device-scope atomic) resolves them.
 // Many rows: one CTA per row does everything.  No host synchronisation; launch shapes depend
 // only on (rows, width, splits), so the whole path can be captured in a hipGraph.
+#include <mutex>
+
 #include "dsa_common.h"
 
 namespace dsa {
@@ -1582,4 +1584,68 @@ extern "C" int dsa_topk_transform_pre(const float* score, int64_t score_stride, 
   return topk_common(score, score_stride, width, mask, mask_stride, lengths, rows, page_table, pt_stride, pt_cols,
                      cu_seqlens_q, n_req, max_splits, n_cu, hist_ws, pass1_done != 0, workspace, workspace_bytes, out,
                      stream, "dsa_topk_transform_pre");
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free variant of dsa_topk_transform: the split path's workspace is a file-scope
+// device array instead of a caller buffer.  Each device holds its own copy of the array until
+// the process ends; its device address is looked up once per device (hipGetSymbolAddress, with
+// that device current) and kept.  The host-side name `scratch` is only a stand-in for the
+// symbol: host code passes the looked-up address, never the array itself.  Every call on one
+// device shares that device's array (the split counters in it are cleared by a fill kernel at
+// the start of each call), so calls that overlap on one device race.
+namespace dsa {
+namespace {
+
+// the split workspace (ws_layout) of up to 256 rows: counters, then candidate keys and tokens
+constexpr size_t kScratchRows = 256;
+constexpr size_t kScratchBytes = (kScratchRows * 16 + 255) / 256 * 256 + 2 * kScratchRows * kCapS * 4;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** ptr, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DSA_ERR_LAUNCH, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DSA_ERR_INVALID, "%s: device ordinal %d out of range", who, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(DSA_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch): %s", who, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return DSA_OK;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" size_t dsa_topk_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int dsa_topk_transform_noalloc(const float* score, int64_t score_stride, int64_t width,
+                                          const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
+                                          int64_t rows, const int32_t* page_table, int64_t pt_stride, int64_t pt_cols,
+                                          const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                                          int32_t* out, hipStream_t stream) {
+  const char* who = "dsa_topk_transform_noalloc";
+  DSA_REQUIRE(rows >= 0 && rows <= 0x7FFFFFFF && width >= 0 && width <= 0x7FFFFFFF, "%s: rows / width out of range",
+              who);
+  const size_t need = dsa_topk_workspace_bytes(rows, width, max_splits, n_cu);
+  if (need > kScratchBytes)
+    return fail(DSA_ERR_WORKSPACE, "%s: %lld rows of width %lld need a %zu-byte split workspace, above the %zu bytes "
+                "of the built-in one (use dsa_topk_transform with a caller workspace, or max_splits = 1)",
+                who, static_cast<long long>(rows), static_cast<long long>(width), need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_address(&ws, who);
+    if (st != DSA_OK) return st;
+  }
+  return topk_common(score, score_stride, width, mask, mask_stride, lengths, rows, page_table, pt_stride, pt_cols,
+                     cu_seqlens_q, n_req, max_splits, n_cu, nullptr, false, ws, need, out, stream, who);
 }

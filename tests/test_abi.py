@@ -30,7 +30,8 @@ def test_header_declares_the_path():
     for n in ["dsa_dequant_k_paged", "dsa_gather_k_paged", "dsa_dequant_mla_paged", "dsa_quant_q_fp8",
               "dsa_store_k_cache", "dsa_mqa_logits_decode", "dsa_mqa_logits_prefill", "dsa_topk_workspace_bytes",
               "dsa_topk_transform", "dsa_topk_transform_pre", "dsa_topk_split_count", "dsa_prefill_slab_rows",
-              "dsa_prefill_indexer_workspace_bytes", "dsa_prefill_indexer", "dsa_last_error", "dsa_device_cu_count"]:
+              "dsa_prefill_indexer_workspace_bytes", "dsa_prefill_indexer", "dsa_topk_transform_noalloc",
+              "dsa_topk_noalloc_max_bytes", "dsa_last_error", "dsa_device_cu_count"]:
         assert n in names
 
 
@@ -135,3 +136,20 @@ def test_reference_knob_gate(monkeypatch):
     assert hcu_ops._topk_splits(32, 16384) == 1
     assert hcu_ops._topk_splits(1, 4096) == 1
     assert hcu_ops._topk_splits(600, 65536) == 1
+
+
+def test_noalloc_topk_rejects_oversize_on_the_host(lib):
+    """The allocation-free top-k refuses inputs whose split workspace exceeds its built-in array,
+    before touching a device: 300 rows of 64K split in two need ~9.8 MB."""
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.dsa_topk_noalloc_max_bytes.restype = ctypes.c_size_t
+    lib.dsa_topk_workspace_bytes.argtypes = [I64, I64, I, I]
+    lib.dsa_topk_workspace_bytes.restype = ctypes.c_size_t
+    cap = lib.dsa_topk_noalloc_max_bytes()
+    assert cap == 4096 + 2 * 256 * 4096 * 4
+    assert lib.dsa_topk_workspace_bytes(256, 65536, 8, 256) == cap
+    assert lib.dsa_topk_workspace_bytes(300, 65536, 8, 256) > cap
+    f = lib.dsa_topk_transform_noalloc
+    f.argtypes = [P, I64, I64, P, I64, P, I64, P, I64, I64, P, I64, I, I, P, P]
+    assert f(P(16), 65536, 65536, None, 0, P(16), 300, P(16), 65536, 65536, None, 300, 8, 256, P(16), None) == 2
+    assert "built-in" in _err(lib)
