@@ -348,6 +348,38 @@ def kernel_time_ms(fn, torch, reps=20, rounds=5, settle_ms=50.0):
     return times[len(times) // 2]
 
 
+def mfma_ceiling(torch, dev, ctas=2048, iters=2000, reps=5):
+    """Measured fp8 MFMA ceilings of this chip (the library's MFMA probe on random non-NaN fp8
+    codes, HIP events on the launch stream, median of `reps` launches after a warm-up one): MFMA
+    alone, and MFMA with the logits epilogue's 8 VALU operations per MFMA; plus the shader clock."""
+    import hcu_ops
+    g = torch.Generator().manual_seed(0)
+    codes = torch.randint(0, 254, (4 * 16384,), generator=g, dtype=torch.int32)
+    codes = (codes + (codes >= 0x7F).int()).to(torch.uint8)  # skips 0x7F; 0xFF is never drawn (NaNs)
+    ops = codes.view(torch.int32).to(dev)
+    flop = ctas * 4 * iters * 8 * 65536.0
+    out = {"unit": "TFLOP/s", "probe": f"{ctas} CTAs x 4 waves x {iters} x 8 v_mfma_f32_16x16x128_f8f6f4, "
+                                      "random fp8 operands"}
+    for name, epi in (("mfma_only", False), ("mfma_with_epilogue_valu", True)):
+        times = []
+        clocks = None
+        for _ in range(reps + 1):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            _, clocks = hcu_ops._C.mfma_fp8_probe(ops, ctas, iters, epi)
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        times = sorted(times[1:])
+        ms = times[len(times) // 2]
+        out[name] = round(flop / (ms / 1e3) / 1e12, 1)
+        c = clocks.cpu().tolist()
+        if c[1] > 0:
+            out[f"{name}_shader_clock_ghz"] = round(c[0] / c[1] * 0.1, 3)
+    return out
+
+
 def cpu_threads(torch):
     """The CPU baseline's threads: torch.set_num_threads(os.cpu_count()), as specified for the
     baseline; the CPUs the process may run on are reported beside it."""
@@ -427,6 +459,12 @@ def run_indexer(name, args, torch, dev, steps=None):
                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
                     "traffic": traffic, "traffic_source": tsrc, "algorithmic_flops": kf,
                     "kernel_us": round(k_ms * 1e3, 2)}
+        measured = mfma_ceiling(torch, dev)
+        measured["logits_frac_of_mfma_only"] = round(achieved / measured["mfma_only"], 4)
+        measured["logits_frac_of_mfma_with_epilogue_valu"] = round(achieved / measured["mfma_with_epilogue_valu"], 4)
+        roofline["measured_ceiling"] = measured
+        log(f"{name}: measured fp8 MFMA ceiling {measured['mfma_only']} TFLOP/s alone, "
+            f"{measured['mfma_with_epilogue_valu']} with the epilogue's VALU work")
         pf = step.path_flops()
         pa = pf / (ms / 1e3) / 1e12
         path = {"bound": "mfma", "achieved": round(pa, 1), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",

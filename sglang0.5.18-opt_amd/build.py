@@ -20,7 +20,8 @@ OBJ = os.path.join(HERE, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["status.cpp", "dequant.hip", "quant.hip", "mqa_logits_decode.hip", "topk.hip", "prefill_indexer.cpp"]
+HIP_SOURCES = ["status.cpp", "dequant.hip", "quant.hip", "mqa_logits_decode.hip", "topk.hip", "prefill_indexer.cpp",
+               "mfma_probe.hip"]
 # Packed fp32 VALU ops (v_pk_fma_f32 and friends) are switched off for every HIP source.  MFMA
 # results are written to VGPRs directly (the epilogues read them with VALU ops; the AGPR form
 # would add one v_accvgpr_read per result element).

@@ -31,13 +31,23 @@ def test_header_declares_the_path():
               "dsa_store_k_cache", "dsa_mqa_logits_decode", "dsa_mqa_logits_prefill", "dsa_topk_workspace_bytes",
               "dsa_topk_transform", "dsa_topk_transform_pre", "dsa_topk_split_count", "dsa_prefill_slab_rows",
               "dsa_prefill_indexer_workspace_bytes", "dsa_prefill_indexer", "dsa_topk_transform_noalloc",
-              "dsa_topk_noalloc_max_bytes", "dsa_last_error", "dsa_device_cu_count"]:
+              "dsa_topk_noalloc_max_bytes", "dsa_last_error", "dsa_device_cu_count", "dsa_mfma_fp8_probe"]:
         assert n in names
 
 
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_functions():
         assert hasattr(lib, name), f"{name} declared in include/dsa_indexer.h but not exported"
+
+
+def test_mfma_probe_rejects_bad_arguments_on_the_host(lib):
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    f = lib.dsa_mfma_fp8_probe
+    f.argtypes = [P, I64, P, P, I, I, I, P]
+    assert f(P(16), 16383, P(16), P(16), 8, 10, 0, None) == 1
+    assert "16384" in _err(lib)
+    assert f(None, 16384, P(16), P(16), 8, 10, 0, None) == 1
+    assert f(P(16), 16384, P(16), P(16), 0, 10, 0, None) == 1
 
 
 def _err(lib):

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 import hcu_ops
+from hcu_ops import _C
 import workloads as wl
 from oracle import indexer as O
 from oracle.topk_c import topk_radix
@@ -248,3 +249,18 @@ def test_prefill_wide_block_nontemporal_stores(gpu):
         L = int(case.lens[r])
         check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
         assert np.isnan(got[r, L:]).all(), f"row {r}: entries past len written"
+
+
+def test_mfma_probe_runs_on_random_fp8(gpu):
+    """The MFMA throughput probe the bench reports beside the published fp8 peak: both modes run,
+    keep finite results and read both clocks."""
+    g = torch.Generator().manual_seed(5)
+    codes = torch.randint(0, 254, (4 * 16384,), generator=g, dtype=torch.int32)
+    codes = (codes + (codes >= 0x7F).int()).to(torch.uint8)
+    ops = codes.view(torch.int32).to(gpu)
+    for epi in (False, True):
+        sink, clocks = _C.mfma_fp8_probe(ops, 64, 20, epi)
+        torch.cuda.synchronize()
+        assert torch.isfinite(sink).all(), f"epilogue={epi}"
+        c = clocks.cpu().tolist()
+        assert c[0] > 0 and c[1] > 0, f"epilogue={epi}: clocks {c}"
