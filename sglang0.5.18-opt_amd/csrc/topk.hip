@@ -444,9 +444,12 @@ __device__ __forceinline__ void sample_issue(const RowSrc& r, SampleLoads<NT>& x
 }
 
 // K* of row r and the candidate digit from its issued sample (block-uniform; every CTA of the
-// row computes the same).
-template <int NT>
-__device__ __forceinline__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x, const SampleLds& S) {
+// row computes the same).  after_sample() runs once every wave holds its share of the sample
+// (right after the barrier that follows its first use): the caller issues its streaming loads
+// there, so that the sample does not wait behind them in the memory queues.
+template <int NT, typename After>
+__device__ __forceinline__ SampleCut sample_threshold(const RowSrc& r, const SampleLoads<NT>& x, const SampleLds& S,
+                                                      After after_sample) {
   constexpr int QPT = SampleLoads<NT>::QPT;
   const int tid = threadIdx.x;
   const Quad* q = x.q;
@@ -462,6 +465,7 @@ __device__ __forceinline__ SampleCut sample_threshold(const RowSrc& r, const Sam
       if ((v[j] >> e) & 1u) atomicAdd(&S.hist[k[j][e] >> 20], 1);
   }
   __syncthreads();
+  after_sample();
   const int rank = sample_rank(r.len);
   const int needs[2] = {rank, sample_mid_rank(r.len)};
   find_thresholds<kBins, NT, 2>(S.hist, needs, S.wtot, S.res);
@@ -1110,10 +1114,11 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
     SampleLoads<kTs> smp;
     sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
     Batch x0, x1;
-    load_batch<kVec, kTs>(r, b0, x0);
-    load_batch<kVec, kTs>(r, b0 + kStep, x1);
     const SampleLds S{L.hist, L.wtot, L.res};
-    const SampleCut cut = sample_threshold<kTs>(r, smp, S);
+    const SampleCut cut = sample_threshold<kTs>(r, smp, S, [&]() {
+      load_batch<kVec, kTs>(r, b0, x0);
+      load_batch<kVec, kTs>(r, b0 + kStep, x1);
+    });
     if (threadIdx.x == 0) L.misc[2] = 0;
     __syncthreads();
     collect_ge<kVec, kTs>(r, b0, (len + kStep - 1) / kStep, cut.thr, L.ck, L.ci, &L.misc[2], kCapS, x0, x1);
@@ -1264,11 +1269,12 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
     SampleLoads<kTs> smp;
     sample_issue<kVec, kTs>(r, smp);  // the sample first: it is needed first
     Batch x0, x1;
-    load_batch<kVec, kTs>(rr, b0, x0);
-    load_batch<kVec, kTs>(rr, b0 + kStep, x1);
     if (tid == 0) L.n[0] = 0;
     const SampleLds S{L.u.res.hist, L.wtot, L.res};
-    const SampleCut cut = sample_threshold<kTs>(r, smp, S);
+    const SampleCut cut = sample_threshold<kTs>(r, smp, S, [&]() {
+      load_batch<kVec, kTs>(rr, b0, x0);
+      load_batch<kVec, kTs>(rr, b0 + kStep, x1);
+    });
     collect_ge<kVec, kTs>(rr, b0, (end - begin + kStep - 1) / kStep, cut.thr, L.u.col.ck, L.u.col.ci, &L.n[0], kCapS,
                           x0, x1);
     __syncthreads();
