@@ -145,7 +145,9 @@ int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int heads, int64_t
  * (bits(x) & 0x80000000) ? ~bits(x) : bits(x) | 0x80000000 (sparse_mask_topk.cu:40-43).
  * The page-table row pr of score row r is r when cu_seqlens_q == NULL (decode layout), else the
  * request b with cu_seqlens_q[b] <= r < cu_seqlens_q[b+1] (n_req + 1 entries; varlen prefill).
- * Only the selected set is the contract; the order within a row is unspecified.
+ * Order within a row (the reference single kernel's, sparse_mask_topk.cu:301-345): the tokens whose
+ * key is above the threshold in ascending token order, then the ties taken, ascending; a function of
+ * the scores alone, the same on every run and graph replay.
  * score f32 [rows, width] row stride score_stride; mask i16 [rows, ceil(width/16)] row stride
  * mask_stride; lengths i32 [rows]; page_table i32 with pt_cols entries per row (tokens at or past
  * pt_cols map to -1) and row stride pt_stride (0: every row reads the same page-table row, e.g.

@@ -72,13 +72,17 @@ __device__ __forceinline__ void load_quad(const RowSrc& r, int i0, Quad& q) {
     q.v[2] = f[2];
     q.v[3] = f[3];
   } else {
+    // 32-bit byte offsets from the row's (wave-uniform) base: scalar-base loads, no 64-bit
+    // address per element
+    const uint32_t last = static_cast<uint32_t>(r.len - 1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = safe + j;
-      q.v[j] = r.vals[t < r.len ? t : r.len - 1];
+      const uint32_t t = min(static_cast<uint32_t>(safe + j), last);
+      q.v[j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(r.vals) + t * 4u);
     }
   }
-  q.mw = static_cast<uint16_t>(r.mask[safe >> 4]);  // unconditional: a dummy word without a mask
+  // no mask (mask_or all ones, wave-uniform): no load at all
+  q.mw = r.mask_or == 0xFFFFu ? static_cast<uint16_t>(0) : static_cast<uint16_t>(r.mask[safe >> 4]);
 }
 
 // Keys of a loaded quad (masked-out tokens are +0) and the bitmask of its tokens below r.len.
@@ -213,7 +217,10 @@ struct PtRow {
   const int32_t* p;
   int cols;
   __device__ __forceinline__ int32_t operator[](int t) const {
-    return static_cast<unsigned>(t) < static_cast<unsigned>(cols) ? p[t] : -1;
+    // a 32-bit byte offset from the row's base (cols < 2^29 by the width limit)
+    return static_cast<unsigned>(t) < static_cast<unsigned>(cols)
+               ? *reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(p) + static_cast<uint32_t>(t) * 4u)
+               : -1;
   }
 };
 
