@@ -351,7 +351,8 @@ def kernel_time_ms(fn, torch, reps=20, rounds=5, settle_ms=50.0):
 def mfma_ceiling(torch, dev, ctas=2048, iters=2000, reps=5):
     """Measured fp8 MFMA ceilings of this chip (the library's MFMA probe on random non-NaN fp8
     codes, HIP events on the launch stream, median of `reps` launches after a warm-up one): MFMA
-    alone, and MFMA with the logits epilogue's 8 VALU operations per MFMA; plus the shader clock."""
+    alone, and MFMA with 4, 8 (the logits epilogue's count) and 16 VALU operations of the
+    epilogue's kind per MFMA; plus the shader clock."""
     import hcu_ops
     g = torch.Generator().manual_seed(0)
     codes = torch.randint(0, 254, (4 * 16384,), generator=g, dtype=torch.int32)
@@ -360,7 +361,8 @@ def mfma_ceiling(torch, dev, ctas=2048, iters=2000, reps=5):
     flop = ctas * 4 * iters * 8 * 65536.0
     out = {"unit": "TFLOP/s", "probe": f"{ctas} CTAs x 4 waves x {iters} x 8 v_mfma_f32_16x16x128_f8f6f4, "
                                       "random fp8 operands"}
-    for name, epi in (("mfma_only", False), ("mfma_with_epilogue_valu", True)):
+    for name, epi in (("mfma_only", 0), ("mfma_with_4_valu", 4), ("mfma_with_epilogue_valu", 8),
+                      ("mfma_with_16_valu", 16)):
         times = []
         clocks = None
         for _ in range(reps + 1):

@@ -222,8 +222,9 @@ int dsa_prefill_indexer(const uint8_t* q8, const float* w, int heads, int64_t ro
  * measured ceiling beside the published dense fp8 peak that the prefill logits are set against.
  * ctas CTAs of 256 threads each run `iters` rounds of 8 independent
  * v_mfma_f32_16x16x128_f8f6f4 (65,536 flop each) on operands read from `operands` (>= 16,384
- * int32 words of fp8 codes, 4 per word; pass random non-NaN codes); with epilogue != 0 every
- * MFMA result also takes the logits epilogue's 8 VALU operations (ReLU + FMA per element).
+ * int32 words of fp8 codes, 4 per word; pass random non-NaN codes); epilogue = VALU operations
+ * each MFMA result takes, of the logits epilogue's kind (ReLU + FMA per element): 0, 4, 8 or 16
+ * (1 = 8, the logits epilogue's count).
  * flop per launch = ctas * 4 * iters * 8 * 65536.  sink: float [ctas * 256] (keeps the work
  * live); clocks: uint64 [2] = shader-clock ticks and 100 MHz ticks of CTA 0's loop. */
 int dsa_mfma_fp8_probe(const int32_t* operands, int64_t n_words, float* sink, uint64_t* clocks, int ctas, int iters,

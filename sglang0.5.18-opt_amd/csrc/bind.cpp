@@ -366,7 +366,7 @@ int64_t prefill_slab_rows(int64_t rows, int64_t width, int64_t memory_budget_byt
 
 // fp8 MFMA throughput probe (a diagnostic): one launch on the current stream; returns the sink
 // float [ctas * 256] and the clocks int64 [2] (shader-clock ticks, 100 MHz ticks of CTA 0).
-std::vector<torch::Tensor> mfma_fp8_probe(const torch::Tensor& operands, int64_t ctas, int64_t iters, bool epilogue) {
+std::vector<torch::Tensor> mfma_fp8_probe(const torch::Tensor& operands, int64_t ctas, int64_t iters, int64_t epilogue) {
   TORCH_CHECK(operands.is_cuda() && operands.scalar_type() == at::kInt && operands.is_contiguous(),
               "operands must be a contiguous int32 CUDA tensor");
   TORCH_CHECK(ctas >= 1 && ctas <= (1 << 20) && iters >= 1 && iters <= (1 << 24), "bad ctas / iters");
@@ -375,7 +375,7 @@ std::vector<torch::Tensor> mfma_fp8_probe(const torch::Tensor& operands, int64_t
   auto clocks = torch::zeros({2}, operands.options().dtype(at::kLong));
   check_status(dsa_mfma_fp8_probe(operands.data_ptr<int>(), operands.numel(), sink.data_ptr<float>(),
                                   reinterpret_cast<uint64_t*>(clocks.data_ptr<int64_t>()), static_cast<int>(ctas),
-                                  static_cast<int>(iters), epilogue ? 1 : 0, cur_stream()));
+                                  static_cast<int>(iters), static_cast<int>(epilogue), cur_stream()));
   return {sink, clocks};
 }
 
@@ -416,6 +416,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("rows"), py::arg("width"), py::arg("max_splits"), py::arg("n_cu") = 0);
   m.def("prefill_slab_rows", &prefill_slab_rows, "rows per logits slab of prefill_indexer for a byte budget");
   m.def("mfma_fp8_probe", &mfma_fp8_probe,
-        "fp8 MFMA throughput probe: ctas x 4 waves x iters x 8 MFMA 16x16x128 -> (sink, clocks)", py::arg("operands"),
-        py::arg("ctas"), py::arg("iters"), py::arg("epilogue"));
+        "fp8 MFMA throughput probe: ctas x 4 waves x iters x 8 MFMA 16x16x128, `epilogue` VALU operations per "
+        "MFMA (0, 4, 8, 16; 1 = 8) -> (sink, clocks)", py::arg("operands"), py::arg("ctas"), py::arg("iters"),
+        py::arg("epilogue"));
 }

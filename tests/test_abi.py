@@ -48,6 +48,8 @@ def test_mfma_probe_rejects_bad_arguments_on_the_host(lib):
     assert "16384" in _err(lib)
     assert f(None, 16384, P(16), P(16), 8, 10, 0, None) == 1
     assert f(P(16), 16384, P(16), P(16), 0, 10, 0, None) == 1
+    assert f(P(16), 16384, P(16), P(16), 8, 10, 3, None) == 1  # 3 VALU operations per MFMA: not a probe mode
+    assert "epilogue" in _err(lib)
 
 
 def _err(lib):
