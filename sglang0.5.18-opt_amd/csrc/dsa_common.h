@@ -21,6 +21,9 @@ constexpr int kBins = 4096;                     // 12-bit radix digit
 constexpr uint32_t kZeroKey = 0x80000000u;      // key of +0.0 (and of masked-out tokens)
 constexpr int kZeroBin = static_cast<int>(kZeroKey >> 20);
 constexpr int kHistWsPerRow = 2 * kBins + 2;    // [ghist1 | ghist2 | (positives, zeros)]
+// Word 3 of a raw buffer descriptor on gfx9-family chips (gfx950): 32-bit data format, no
+// swizzle; with stride 0 a load whose byte offset is at or past num_records returns 0.
+constexpr int kBufferDword3 = 0x00020000;
 
 // ------------------------------------------------------------------------------------------
 // Order-preserving float -> uint32 key (sparse_mask_topk.cu:40-43): larger float, larger key;

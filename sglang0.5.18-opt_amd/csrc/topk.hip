@@ -72,17 +72,24 @@ __device__ __forceinline__ void load_quad(const RowSrc& r, int i0, Quad& q) {
     q.v[2] = f[2];
     q.v[3] = f[3];
   } else {
-    // 32-bit byte offsets from the row's (wave-uniform) base: scalar-base loads, no 64-bit
-    // address per element
-    const uint32_t last = static_cast<uint32_t>(r.len - 1);
+    // raw buffer loads against a descriptor of the row (base and size wave-uniform): one 32-bit
+    // offset per token, and tokens past r.len read 0 (the descriptor's range check), not memory
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(r.vals), 0, static_cast<int>(static_cast<uint32_t>(r.len) * 4u), kBufferDword3);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t t = min(static_cast<uint32_t>(safe + j), last);
-      q.v[j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(r.vals) + t * 4u);
-    }
+    for (int j = 0; j < 4; ++j)
+      q.v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (safe + j) * 4, 0, 0));
   }
   // no mask (mask_or all ones, wave-uniform): no load at all
-  q.mw = r.mask_or == 0xFFFFu ? static_cast<uint16_t>(0) : static_cast<uint16_t>(r.mask[safe >> 4]);
+  if (r.mask_or == 0xFFFFu) {
+    q.mw = 0;
+  } else if constexpr (kVec) {
+    q.mw = static_cast<uint16_t>(r.mask[safe >> 4]);
+  } else {
+    const __amdgpu_buffer_rsrc_t ms = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int16_t*>(r.mask), 0, static_cast<int>((static_cast<uint32_t>(r.len) + 15u) >> 4) * 2, kBufferDword3);
+    q.mw = __builtin_amdgcn_raw_buffer_load_b16(ms, (safe >> 4) * 2, 0, 0);
+  }
 }
 
 // Keys of a loaded quad (masked-out tokens are +0) and the bitmask of its tokens below r.len.
@@ -1115,7 +1122,9 @@ __global__ __launch_bounds__(kTs) __attribute__((amdgpu_waves_per_eu(4))) void t
   const RowSrc r = row_src(a, row, len);
   bool done = false;
   if (len <= kSample) {  // block-uniform
-    done = small_row<kVec, kTs>(L, r, pt, dst);
+    // unaligned rows (scalar loads) take the exact path: small_row beside it would push this
+    // variant past 128 VGPRs into scratch
+    if constexpr (kVec) done = small_row<kVec, kTs>(L, r, pt, dst);
   } else {
     const int b0 = static_cast<int>(threadIdx.x) * 4;
     SampleLoads<kTs> smp;

@@ -86,11 +86,13 @@ def test_topk_zero_negative_and_short_lengths(gpu):
         assert np.array_equal(got, ref), f"impl={name}"
 
 
+@pytest.mark.parametrize("L", [30000, 3500])
 @pytest.mark.parametrize("extra", [36, 37])
-def test_topk_strided_score_mask_and_page_table(gpu, extra):
+def test_topk_strided_score_mask_and_page_table(gpu, extra, L):
     """Score, mask and page-table rows that are views into wider buffers: row strides above the
-    width (extra % 4 == 0 keeps the 16-B score loads, 37 takes the scalar path)."""
-    B, L = 6, 30000
+    width (extra % 4 == 0 keeps the 16-B score loads, 37 takes the scalar path: buffer loads,
+    rows of <= 4096 tokens on the exact path)."""
+    B = 6
     W = L + 64
     x, mask, lengths, pt = wl.topk_scores(B, L, "mixed", W=W, ragged=True, seed=7)
     ref = topk_radix(x.numpy(), mask.numpy(), lengths.numpy(), pt.numpy(), W)
