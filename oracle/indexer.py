@@ -55,15 +55,19 @@ def dequant_k_paged(kv, slots):
 
 def dequant_mla(cache, slots):
     """bf16 bits [n, 576] of the 656-B MLA slot (dequant_k_cache.py.diff:16-42,56-62):
-    [0:512] = bf16_rne(f32(fp8[j]) * scale[j // 128]), [512:576] = the bf16 rope copy."""
+    [0:512] = bf16_rne(f32(fp8[j]) * scale[j // 128]), [512:576] = the bf16 rope copy.  A
+    negative slot (a padded entry, which the reference's kernel would read out of bounds) gives
+    a zero row, as in dequant_k_paged."""
     slots = np.asarray(slots, dtype=np.int64)
-    rows = cache[slots]
+    rows = cache[np.maximum(slots, 0)]
     codes = rows[:, :512]
     scale = np.ascontiguousarray(rows[:, 512:528]).view(np.float32).reshape(-1, 4)
     vals = fp8_decode(codes).reshape(-1, 4, 128) * scale[:, :, None]
     nope = bf16_rne(vals.reshape(-1, 512).astype(np.float32))
     rope = np.ascontiguousarray(rows[:, 528:656]).view(np.uint16).reshape(-1, 64)
-    return np.concatenate([nope, rope], axis=1)
+    out = np.concatenate([nope, rope], axis=1)
+    out[slots < 0] = 0
+    return out
 
 
 # --------------------------------------------------------------------------------------------

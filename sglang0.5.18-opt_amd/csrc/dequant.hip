@@ -1,8 +1,9 @@
-// Paged K-cache gather / dequant kernels (HBM-bound, 128-bit loads and stores).
+// Paged K-cache gather / dequant kernels (HBM-bound; each wave-wide load or store covers one
+// contiguous span: 8 fp8 bytes in, 16 bf16 bytes out per lane).
 //
-//   dequant_k_kernel   indexer 132-B layout -> bf16 [n, 128]
+//   dequant_k_kernel   indexer 132-B layout -> bf16 [n, 128] (16 lanes per token)
 //   gather_k_kernel    indexer 132-B layout -> contiguous fp8 [n, 128] + fp32 scale [n]
-//   dequant_mla_kernel MLA 656-B slot -> bf16 [n, 576]
+//   dequant_mla_kernel MLA 656-B slot -> bf16 [n, 576] (a wave per token)
 //
 // Numerics (prefill/patches/dequant_k_cache.py.diff:30-36): f32(fp8) is exact, one fp32
 // multiply by the token's (group's) scale, one round-to-nearest-even to bf16 (NaN -> 0x7FC0).
@@ -14,46 +15,75 @@ namespace dsa {
 namespace {
 
 using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
 
-// 16 fp8 bytes * s -> 16 bf16 (8 words).
-__device__ __forceinline__ void dequant16(const u32x4 q, float s, u32x4& lo, u32x4& hi) {
-  uint32_t out[8];
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const int v = static_cast<int>(q[w]);
-    const auto f01 = __builtin_amdgcn_cvt_pk_f32_fp8(v, false);
-    const auto f23 = __builtin_amdgcn_cvt_pk_f32_fp8(v, true);
-    out[2 * w] = bf16_rne_bits(f01[0] * s) | (bf16_rne_bits(f01[1] * s) << 16);
-    out[2 * w + 1] = bf16_rne_bits(f23[0] * s) | (bf16_rne_bits(f23[1] * s) << 16);
-  }
-  lo = u32x4{out[0], out[1], out[2], out[3]};
-  hi = u32x4{out[4], out[5], out[6], out[7]};
+// 8 fp8 bytes * s -> 8 bf16 (4 words).
+__device__ __forceinline__ u32x4 dequant8(const u32x2 q, float s) {
+  const auto f01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(q[0]), false);
+  const auto f23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(q[0]), true);
+  const auto f45 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(q[1]), false);
+  const auto f67 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(q[1]), true);
+  return u32x4{bf16_rne_bits(f01[0] * s) | (bf16_rne_bits(f01[1] * s) << 16),
+               bf16_rne_bits(f23[0] * s) | (bf16_rne_bits(f23[1] * s) << 16),
+               bf16_rne_bits(f45[0] * s) | (bf16_rne_bits(f45[1] * s) << 16),
+               bf16_rne_bits(f67[0] * s) | (bf16_rne_bits(f67[1] * s) << 16)};
+}
+
+template <bool kNt>
+__device__ __forceinline__ void store16(uint16_t* p, const u32x4 v) {
+  if constexpr (kNt) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+  else *reinterpret_cast<u32x4*>(p) = v;
+}
+
+template <bool kNt>
+__device__ __forceinline__ void store4(uint16_t* p, uint32_t v) {
+  if constexpr (kNt) __builtin_nontemporal_store(v, reinterpret_cast<uint32_t*>(p));
+  else *reinterpret_cast<uint32_t*>(p) = v;
 }
 
 constexpr int kDqThreads = 256;
 constexpr int kChunksPerTok = kHeadDim / 16;  // 8 x 16 B per token
 
-// Thread t of the grid handles 16-byte chunk (t % 8) of token (t / 8).
+// 16 lanes per token, 4 tokens a wave: lane j of a token's 16 dequantises its fp8 bytes 8j .. 8j + 7
+// into output bytes 16j .. 16j + 15 (a wave's store: the 1 KB of 4 output rows).  A wave takes
+// kKQuads groups of 4 tokens a pass, n_waves groups apart, their loads issued together; the
+// launch gives every wave one pass.
+constexpr int kKQuads = 2;
+
+template <bool kNtOut>
 __global__ __launch_bounds__(kDqThreads) void dequant_k_kernel(
     const uint8_t* __restrict__ kv, int64_t page_stride, const int32_t* __restrict__ slots,
     int64_t n, uint16_t* __restrict__ out, int64_t out_stride) {
-  const int64_t total = n * kChunksPerTok;
-  for (int64_t g = static_cast<int64_t>(blockIdx.x) * kDqThreads + threadIdx.x; g < total;
-       g += static_cast<int64_t>(gridDim.x) * kDqThreads) {
-    const int64_t tok = g >> 3;
-    const int c = static_cast<int>(g & 7);
-    const int32_t slot = slots[tok];
-    u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-    if (slot >= 0) {
-      const uint8_t* page = kv + static_cast<int64_t>(slot >> 6) * page_stride;
-      const int off = slot & (kPage - 1);
-      const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(page + off * kHeadDim + c * 16));
-      const float s = *reinterpret_cast<const float*>(page + kPageFp8Bytes + off * 4);
-      dequant16(q, s, lo, hi);
+  constexpr int U = kKQuads;
+  constexpr int kWavesPerCta = kDqThreads / kWave;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & 15;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * kWavesPerCta;
+  const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kWavesPerCta + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int64_t g0 = w0; g0 * 4 < n; g0 += n_waves * U) {  // wave-uniform
+    int64_t tok[U];
+    int32_t sl[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      tok[u] = (g0 + u * n_waves) * 4 + (lane >> 4);
+      sl[u] = tok[u] < n ? slots[tok[u]] : -1;
     }
-    u32x4* o = reinterpret_cast<u32x4*>(out + tok * out_stride + c * 16);
-    o[0] = lo;
-    o[1] = hi;
+    u32x2 q[U];
+    float s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      q[u] = u32x2{0u, 0u};
+      s[u] = 0.0f;
+      if (sl[u] >= 0) {
+        const uint8_t* page = kv + static_cast<int64_t>(sl[u] >> 6) * page_stride;
+        const int off = sl[u] & (kPage - 1);
+        q[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(page + off * kHeadDim + sub * 8));
+        s[u] = *reinterpret_cast<const float*>(page + kPageFp8Bytes + off * 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (tok[u] < n) store16<kNtOut>(out + tok[u] * out_stride + sub * 8, dequant8(q[u], s[u]));
   }
 }
 
@@ -79,63 +109,55 @@ __global__ __launch_bounds__(kDqThreads) void gather_k_kernel(
   }
 }
 
-// MLA slot: [512 fp8 | 4 x f32 | 64 x bf16] = 656 B.  40 work items per token: 32 dequant
-// chunks of 16 fp8 (group = chunk / 8) and 8 rope chunks of 16 B.
-constexpr int kMlaNope = 512;
+// MLA slot: [512 fp8 | 4 x f32 | 64 x bf16] = 656 B -> bf16 [576].  One wave per token: lane i
+// dequantises fp8 bytes 8i .. 8i + 7 (scale group i / 16) into output bytes 16i .. 16i + 15, and
+// lanes 0-31 copy rope bytes 4i .. 4i + 3 behind them; the token's slot index is a scalar load,
+// so every load and store of the wave covers one contiguous span of the slot or of the output
+// row (one 1 KB store, one 128 B store).  A wave takes kMlaTok tokens a pass, n_waves apart,
+// with every load of the pass issued before the first is used; the launch gives every wave one
+// pass.  kNtOut: the rows are stored nontemporally (an output larger than the MALL).
 constexpr int kMlaScaleOff = 512;
 constexpr int kMlaRopeOff = 528;
-constexpr int kMlaItems = 40;
-constexpr int kMlaUnroll = 4;  // work items per thread per pass, their loads issued together
+constexpr int kMlaTok = 2;
 
-// I: the index type (uint32_t when n * 40 fits, else int64_t).  Each pass takes kMlaUnroll items
-// a grid apart: their slot indices, then their slot bytes, are loaded before any is used, so a
-// thread keeps kMlaUnroll 16-B loads in flight (one dependent slot -> bytes chain per pass).
-template <typename I>
+template <bool kNtOut>
 __global__ __launch_bounds__(kDqThreads) void dequant_mla_kernel(
     const uint8_t* __restrict__ cache, int64_t stride, const int32_t* __restrict__ slots,
     int64_t n, uint16_t* __restrict__ out, int64_t out_stride) {
-  constexpr int U = kMlaUnroll;
-  const I total = static_cast<I>(n * kMlaItems);
-  const I step = static_cast<I>(gridDim.x) * kDqThreads;
-  for (I g0 = static_cast<I>(blockIdx.x) * kDqThreads + threadIdx.x; g0 < total; g0 += step * U) {
-    I tok[U];
-    int c[U];
-    int32_t slot[U];
+  constexpr int U = kMlaTok;
+  constexpr int kWavesPerCta = kDqThreads / kWave;
+  const int lane = threadIdx.x & 63;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * kWavesPerCta;
+  const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kWavesPerCta + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int64_t t0 = w0; t0 < n; t0 += n_waves * U) {  // wave-uniform
+    int32_t sl[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const I g = g0 + u * step;
-      const bool in = g < total;
-      tok[u] = in ? g / kMlaItems : 0;
-      c[u] = static_cast<int>(g - tok[u] * kMlaItems);
-      slot[u] = in ? slots[tok[u]] : -1;
+      const int64_t t = t0 + u * n_waves;
+      sl[u] = t < n ? slots[t] : -1;
     }
-    u32x4 v[U];
+    u32x2 q[U];
     float s[U];
+    uint32_t rp[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      v[u] = u32x4{0u, 0u, 0u, 0u};
+      q[u] = u32x2{0u, 0u};
       s[u] = 0.0f;
-      if (slot[u] >= 0) {
-        const uint8_t* src = cache + static_cast<int64_t>(slot[u]) * stride;
-        const bool nope = c[u] < 32;
-        v[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(src + (nope ? c[u] * 16 : kMlaRopeOff + (c[u] - 32) * 16)));
-        if (nope) s[u] = *reinterpret_cast<const float*>(src + kMlaScaleOff + (c[u] >> 3) * 4);
+      rp[u] = 0u;
+      if (sl[u] >= 0) {  // wave-uniform
+        const uint8_t* src = cache + static_cast<int64_t>(sl[u]) * stride;
+        q[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + lane * 8));
+        s[u] = *reinterpret_cast<const float*>(src + kMlaScaleOff + (lane >> 4) * 4);
+        if (lane < 32) rp[u] = *reinterpret_cast<const uint32_t*>(src + kMlaRopeOff + lane * 4);
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (g0 + u * step >= total) break;
-      uint16_t* dst = out + static_cast<int64_t>(tok[u]) * out_stride;
-      if (c[u] < 32) {
-        u32x4 lo, hi;
-        dequant16(v[u], s[u], lo, hi);
-        u32x4* o = reinterpret_cast<u32x4*>(dst + c[u] * 16);
-        o[0] = lo;
-        o[1] = hi;
-      } else {
-        *reinterpret_cast<u32x4*>(dst + kMlaNope + (c[u] - 32) * 8) = v[u];
-      }
+      const int64_t t = t0 + u * n_waves;
+      if (t >= n) break;
+      uint16_t* dst = out + t * out_stride;
+      store16<kNtOut>(dst + lane * 8, dequant8(q[u], s[u]));
+      if (lane < 32) store4<kNtOut>(dst + 512 + lane * 2, rp[u]);
     }
   }
 }
@@ -163,8 +185,15 @@ extern "C" int dsa_dequant_k_paged(const uint8_t* kv_cache, int64_t page_stride_
               "dsa_dequant_k_paged: pages must be >= 8448 B, 16-B aligned (page_stride %% 16 == 0)");
   DSA_REQUIRE(out_stride >= kHeadDim && out_stride % 8 == 0 && aligned16(out),
               "dsa_dequant_k_paged: out must be 16-B aligned with out_stride %% 8 == 0 and >= 128");
-  hipLaunchKernelGGL(dequant_k_kernel, dim3(grid_for(n_tokens * kChunksPerTok)), dim3(kDqThreads), 0,
-                     stream, kv_cache, page_stride_bytes, slots, n_tokens, out, out_stride);
+  const int64_t ctas = ((n_tokens + 4 * kKQuads - 1) / (4 * kKQuads) + 3) / 4;  // a pass per wave
+  const dim3 grid(static_cast<uint32_t>(ctas < 0x7FFFFFFF ? ctas : 0x7FFFFFFF));
+  if (n_tokens * out_stride * 2 > (256ll << 20)) {  // an output larger than the MALL: nontemporal rows
+    hipLaunchKernelGGL(dequant_k_kernel<true>, grid, dim3(kDqThreads), 0, stream, kv_cache, page_stride_bytes, slots,
+                       n_tokens, out, out_stride);
+  } else {
+    hipLaunchKernelGGL(dequant_k_kernel<false>, grid, dim3(kDqThreads), 0, stream, kv_cache, page_stride_bytes, slots,
+                       n_tokens, out, out_stride);
+  }
   return check_launch("dsa_dequant_k_paged");
 }
 
@@ -193,15 +222,18 @@ extern "C" int dsa_dequant_mla_paged(const uint8_t* cache, int64_t cache_stride_
               "dsa_dequant_mla_paged: slots must be >= 656 B with a 16-B aligned stride");
   DSA_REQUIRE(out_stride >= 576 && out_stride % 8 == 0 && aligned16(out),
               "dsa_dequant_mla_paged: out must be 16-B aligned with out_stride %% 8 == 0 and >= 576");
-  const int64_t items = n_tokens * kMlaItems;
-  // up to 32768 CTAs (a thread's passes then stay few; measured 2% faster than 8192 at 393K tokens)
-  const dim3 grid(grid_for((items + kMlaUnroll - 1) / kMlaUnroll, 32768));
-  if (items + static_cast<int64_t>(grid.x) * kDqThreads * kMlaUnroll <= 0xFFFFFFFFll) {
-    hipLaunchKernelGGL(dequant_mla_kernel<uint32_t>, grid, dim3(kDqThreads), 0, stream, cache, cache_stride_bytes,
-                       slots, n_tokens, out, out_stride);
+  // a wave per kMlaTok tokens, one pass each (measured on 392,832 tokens: 2 tokens a wave 123 us,
+  // 4 127 us, 8 132 us; grids capped at 8192 CTAs with more passes a wave 134 us)
+  const int64_t ctas = ((n_tokens + kMlaTok - 1) / kMlaTok + 3) / 4;
+  const dim3 grid(static_cast<uint32_t>(ctas < 0x7FFFFFFF ? ctas : 0x7FFFFFFF));
+  // nontemporal rows when the output exceeds the 256 MB MALL (392,832 tokens, 453 MB: 141 -> 123
+  // us; 131,072 tokens, 151 MB: 40 us plain, 44 us nontemporal)
+  if (n_tokens * out_stride * 2 > (256ll << 20)) {
+    hipLaunchKernelGGL(dequant_mla_kernel<true>, grid, dim3(kDqThreads), 0, stream, cache, cache_stride_bytes, slots,
+                       n_tokens, out, out_stride);
   } else {
-    hipLaunchKernelGGL(dequant_mla_kernel<int64_t>, grid, dim3(kDqThreads), 0, stream, cache, cache_stride_bytes,
-                       slots, n_tokens, out, out_stride);
+    hipLaunchKernelGGL(dequant_mla_kernel<false>, grid, dim3(kDqThreads), 0, stream, cache, cache_stride_bytes, slots,
+                       n_tokens, out, out_stride);
   }
   return check_launch("dsa_dequant_mla_paged");
 }

@@ -49,7 +49,23 @@ def test_dequant_and_gather_random_cache(gpu):
     assert np.array_equal(sc.cpu().numpy().view(np.uint32), scale.view(np.uint32))
 
 
-@pytest.mark.parametrize("n", [1, 7, 3000, 250000])  # 250000: several grid-stride passes per thread
+def test_dequant_k_large_output(gpu):
+    """2^20 + 1 tokens: a 268 MB output, past the 256 MB at which the rows are stored
+    nontemporally; padded (-1) slots give zero rows."""
+    g = torch.Generator().manual_seed(5)
+    pages = 4096
+    kv = torch.randint(0, 256, (pages, 64 * 132), generator=g, dtype=torch.uint8)
+    kv[:, 8192:] = (torch.rand(pages, 64, generator=g) * 0.05 + 1e-3).view(torch.uint8)
+    n = (1 << 20) + 1
+    slots = torch.randint(0, pages * 64, (n,), generator=g, dtype=torch.int32)
+    slots[::1001] = -1
+    got = hcu_ops.dequant_k_paged(kv.view(pages, 64, 1, 132).to(gpu), slots.to(gpu))
+    ref = O.dequant_k_paged(kv.numpy(), slots.numpy())
+    assert np.array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+# 250000: a 288 MB output (nontemporal rows); negative slots are padded entries (zero rows)
+@pytest.mark.parametrize("n", [1, 7, 3000, 250000])
 def test_dequant_mla_656(gpu, n):
     g = torch.Generator().manual_seed(2)
     pool = 4096
@@ -57,6 +73,7 @@ def test_dequant_mla_656(gpu, n):
     cache[:, 512:528] = (torch.rand(pool, 4, generator=g) * 0.02 + 1e-3).view(torch.uint8)
     cache[:, 528:] = torch.randn(pool, 64, generator=g).to(torch.bfloat16).view(torch.uint8)
     slots = torch.randint(0, pool, (n,), generator=g, dtype=torch.int32)
+    slots[3::53] = -1
     got = hcu_ops.dequantize_k_cache_paged(cache.view(torch.float8_e4m3fn).view(pool, 1, 656).to(gpu), slots.to(gpu))
     assert tuple(got.shape) == (n, 1, 576) and got.dtype == torch.bfloat16
     ref = O.dequant_mla(cache.numpy(), slots.numpy())

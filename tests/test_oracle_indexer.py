@@ -76,6 +76,12 @@ def test_dequant_mla_matches_torch_closed_form():
     ref_nope = (nope * sc[:, :, None]).view(-1, 512).to(torch.bfloat16)
     ref = torch.cat([ref_nope, rows[:, 528:].contiguous().view(torch.bfloat16)], 1)
     assert np.array_equal(got, ref.view(torch.int16).numpy().view(np.uint16))
+    # padded entries (negative slots) are zero rows; the other rows are unchanged
+    neg = slots.clone()
+    neg[::7] = -1
+    got2 = O.dequant_mla(cache.numpy(), neg.numpy())
+    keep = neg.numpy() >= 0
+    assert (got2[~keep] == 0).all() and np.array_equal(got2[keep], got[keep])
 
 
 def test_quant_vectors_matches_torch_generator():
