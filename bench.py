@@ -21,6 +21,11 @@ The JSON line also carries
                 *scale -> kthvalue top-2048 -> gather) timed on a bounded sample of the same
                 workload on this host's cores.
 
+The default line (decode_mtp64, the quoted decode configuration, as `value`) also holds one object
+per other configuration -- prefill_8k_64k (the prefill headline), prefill_16k_128k, decode_32x16k,
+decode_1x4k -- and one for dequant_mla_393k (the 656-B MLA dequant), each with its own step time,
+roofline and CPU baseline.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_mtp64]
 """
 import argparse
@@ -498,7 +503,8 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true",
-                    help="the default decode_mtp64 line only (no prefill_8k_64k object)")
+                    help="the default decode_mtp64 line only (no objects for the other workloads)")
+    ap.add_argument("--no-dequant", action="store_true", help="no dequant_mla_393k object in the default line")
     ap.add_argument("--steps-per-graph", type=int, default=10, help="steps captured in one hipGraph")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB three times (the known-size kernel that "
@@ -523,13 +529,13 @@ def main(argv=None):
         log(f"copy calibration: 3 copies of {args.copy_calibration_mib} MiB")
         del src, dst
     if args.workload.startswith("dequant"):
-        t0 = time.perf_counter()
-        case = getattr(wl, args.workload)()
-        log(f"built {args.workload} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
-        step = DequantStep(case, dev)
-        torch.cuda.synchronize()
-        ms, per = timed_steps(step, args, torch)
-        return dequant_report(args, case, step, ms, per, torch)
+        d = run_dequant(args.workload, args, torch, dev)
+        line = {"metric": DEQUANT_METRIC, "value": d["value"], "unit": "GB/s", "n_gpus": 1, "steps": d["steps"],
+                "warmup": d["warmup"], "ms_per_step": d["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+                "vs_baseline": None, "dtype": "fp8e4m3 -> bf16", "data": "synthetic (seeded, see tests/workloads.py)",
+                "config": d["config"], "roofline": d["roofline"], "cpu_baseline": d["cpu_baseline"]}
+        print(json.dumps(line), flush=True)
+        return 0
 
     head = run_indexer(args.workload, args, torch, dev)
     line = {"metric": METRIC, "value": head["value"], "unit": "K-tokens/s", "n_gpus": 1, "steps": head["steps"],
@@ -538,24 +544,35 @@ def main(argv=None):
             "data": "synthetic (seeded, see tests/workloads.py)", "config": head["config"],
             "roofline": head["roofline"], "path_roofline": head["path_roofline"], "cpu_baseline": head["cpu_baseline"]}
     if args.workload == "decode_mtp64" and not args.no_prefill:
-        # the second headline workload (the 64K-prefix chunked prefill) in the same line, its
-        # own step count sized to the same wall time
-        pre = run_indexer("prefill_8k_64k", args, torch, dev,
-                          steps={"steps": max(2, args.steps // 10), "warmup": max(1, args.warmup // 10),
-                                 "steps_per_graph": 1})
-        line["prefill_8k_64k"] = {"metric": METRIC, "unit": "K-tokens/s", **pre}
+        # the second headline workload (the 64K-prefix chunked prefill) and the other configurations
+        # in the same line, each with its own roofline and CPU baseline; prefill step counts sized
+        # to about the same wall time
+        few = {"steps": max(2, args.steps // 10), "warmup": max(1, args.warmup // 10), "steps_per_graph": 1}
+        for name, steps in (("prefill_8k_64k", few), ("prefill_16k_128k", few), ("decode_32x16k", None),
+                            ("decode_1x4k", None)):
+            line[name] = {"metric": METRIC, "unit": "K-tokens/s", **run_indexer(name, args, torch, dev, steps=steps)}
+        if not args.no_dequant:
+            line["dequant_mla_393k"] = {"metric": DEQUANT_METRIC, "unit": "GB/s",
+                                        **run_dequant("dequant_mla_393k", args, torch, dev)}
     print(json.dumps(line), flush=True)
     return 0
 
 
-def dequant_report(args, case, step, ms, per, torch):
-    """The JSON line of a dequant workload: a step is one dequant launch."""
+def run_dequant(name, args, torch, dev):
+    """One dequant workload (a step is one dequant launch) as the fields of a JSON line."""
+    import workloads as wl
+    t0 = time.perf_counter()
+    case = getattr(wl, name)()
+    log(f"built {name} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
+    step = DequantStep(case, dev)
+    torch.cuda.synchronize()
+    ms, per = timed_steps(step, args, torch)
     nb = step.bytes()
     value = nb / (ms / 1e3) / 1e9
     k_ms = kernel_time_ms(step, torch)
     achieved = nb / (k_ms / 1e3) / 1e9
     log(f"timed {args.steps} launches: {ms * 1e3:.1f} us each, {value:.1f} GB/s; graph of 20 alone {k_ms * 1e3:.1f} us")
-    traffic, tsrc = profiled_traffic(step.kernel, args.workload)
+    traffic, tsrc = profiled_traffic(step.kernel, name)
     roofline = {"bound": "hbm", "kernel": step.kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": tsrc,
                 "algorithmic_bytes": nb, "kernel_us": round(k_ms * 1e3, 2)}
@@ -564,17 +581,11 @@ def dequant_report(args, case, step, ms, per, torch):
         v, sample = dequant_cpu_baseline(case, args.cpu_budget, step.tok_bytes)
         cpu = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port", "sample": sample, "cpu": cpu_model()}
         log(f"cpu baseline {v:.3g} GB/s ({sample})")
-    line = {
-        "metric": DEQUANT_METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp8e4m3 -> bf16", "data": "synthetic (seeded, see tests/workloads.py)",
-        "config": {"workload": f"{args.workload}: {WORKLOADS[args.workload]}", "tokens": int(case.tokens),
-                   "bytes_per_token": step.tok_bytes, "graph": f"hipGraph of {per} launches per replay",
-                   "settle_ms": args.settle_ms},
-        "roofline": roofline, "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
-    return 0
+    return {"value": round(value, 1), "ms_per_step": round(ms, 5), "steps": args.steps, "warmup": args.warmup,
+            "config": {"workload": f"{name}: {WORKLOADS[name]}", "tokens": int(case.tokens),
+                       "bytes_per_token": step.tok_bytes, "graph": f"hipGraph of {per} launches per replay",
+                       "settle_ms": args.settle_ms},
+            "roofline": roofline, "cpu_baseline": cpu}
 
 
 if __name__ == "__main__":
