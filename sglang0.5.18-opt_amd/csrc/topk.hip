@@ -191,14 +191,28 @@ __device__ __forceinline__ void find_threshold_regs(const int (&h)[BPT], int nee
   find_thresholds_regs<NT, BPT, 1>(h, n, s_wtot, s_res);
 }
 
-// The same over an LDS histogram of NB bins.
+// The same over an LDS histogram of NB bins (16-B aligned: every histogram here is the first
+// member of an alignas(16) LDS struct).  With at least 4 bins a thread, 16-B reads and no guard
+// (measured: the 64-request MTP top-k 23.0 -> 21.9 us, a 4096-row prefill slab 332 -> 327 us).
 template <int NB, int NT, int NN>
 __device__ __forceinline__ void find_thresholds(const int* hist, const int (&need)[NN], int* s_wtot, int* s_res) {
   constexpr int BPT = NB >= NT ? NB / NT : 1;
   constexpr int ACTIVE = NB / BPT;
   int h[BPT];
+  if constexpr (ACTIVE == NT && BPT % 4 == 0) {
+    const int4* p = reinterpret_cast<const int4*>(__builtin_assume_aligned(hist, 16)) + threadIdx.x * (BPT / 4);
 #pragma unroll
-  for (int j = 0; j < BPT; ++j) h[j] = static_cast<int>(threadIdx.x) < ACTIVE ? hist[threadIdx.x * BPT + j] : 0;
+    for (int j = 0; j < BPT / 4; ++j) {
+      const int4 v = p[j];
+      h[4 * j] = v.x;
+      h[4 * j + 1] = v.y;
+      h[4 * j + 2] = v.z;
+      h[4 * j + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) h[j] = static_cast<int>(threadIdx.x) < ACTIVE ? hist[threadIdx.x * BPT + j] : 0;
+  }
   find_thresholds_regs<NT, BPT, NN>(h, need, s_wtot, s_res);
 }
 
@@ -208,6 +222,7 @@ __device__ __forceinline__ void find_threshold(const int* hist, int need, int* s
   find_thresholds<NB, NT, 1>(hist, n, s_wtot, s_res);
 }
 
+// (16-B stores here measured slower than these 4-B ones: 0.1-2 us more per top-k launch.)
 template <int NT>
 __device__ __forceinline__ void zero_lds(int* p, int n) {
   for (int i = threadIdx.x; i < n; i += NT) p[i] = 0;
