@@ -67,8 +67,9 @@ int dsa_gather_k_paged(const uint8_t* kv_cache, int64_t page_stride_bytes, const
  * slot = [512 fp8][4 x fp32 group scales][64 bf16 rope];
  *   out[i, 0:512]   = bf16_rne(f32(fp8[src, j]) * scale[src, j / 128])
  *   out[i, 512:576] = rope[src]
- * cache: u8 [pool, >=656] with row stride cache_stride_bytes (% 16 == 0); slots int32 [n];
- * out bf16 [n, >=576] with row stride out_stride (elements, % 8 == 0). */
+ * cache: u8 [pool, >=656] with row stride cache_stride_bytes (% 16 == 0); slots int32 [n]
+ * (a negative slot, a padded entry, gives a zero row); out bf16 [n, >=576] with row stride
+ * out_stride (elements, % 8 == 0). */
 int dsa_dequant_mla_paged(const uint8_t* cache, int64_t cache_stride_bytes, const int32_t* slots,
                           int64_t n_tokens, uint16_t* out, int64_t out_stride, hipStream_t stream);
 
