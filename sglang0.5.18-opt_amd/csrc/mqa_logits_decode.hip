@@ -197,10 +197,12 @@ __device__ void assign_cta(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* 
 // each, and the block-table slice a CTA stages (the host keeps P / T within it; it also bounds a
 // row's tokens per CTA below 2^16 for the 16-bit histogram counters).  Measured on the 64-request
 // MTP decode: one stream per CTA (eight CTAs per CU) without the histogram; with it, the 8 KB
-// per row of counters is amortised over two streams (R = 2) or four (R = 1).
+// per row of counters is amortised over two streams (R = 2) or four (R = 1).  One-row CTAs run
+// two streams (half the CTAs to dispatch for the same pages in flight: 32 x 16K decode 16.1 ->
+// 15.7 us, 1 x 4K 6.4 -> 6.3 us; two-row CTAs measured 0.5 us slower with two).
 template <int R, bool kHist>
 struct Shape {
-  static constexpr int S = kHist ? (R == 1 ? 4 : (R == 2 ? 2 : 1)) : 1;
+  static constexpr int S = kHist ? (R == 1 ? 4 : (R == 2 ? 2 : 1)) : (R == 1 ? 2 : 1);
   static constexpr int NS = 2;
   static constexpr int kMaxPages = S == 1 ? 255 : (S == 2 ? 511 : 1023);
   static constexpr int kLds = S * NS * kPageBytes + (kHist ? R * kBins * 2 : 0) + kMaxPages * 4 + 512;
