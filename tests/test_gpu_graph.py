@@ -1,4 +1,4 @@
-"""The decode step under hipGraph capture: captured once on static buffers, replayed with new
+"""The decode step and the prefill indexer under hipGraph capture: captured once on static buffers, replayed with new
 inputs copied into them (new queries, weights, K pages, lengths and block tables of the same
 shapes), each replay bit-identical to an eager run of the same inputs (logits, mask and the
 top-k rows, their order included) and identical to the oracle's selection.  The reference
@@ -84,4 +84,55 @@ def test_decode_step_graph_replay(gpu):
         assert torch.equal(g_out, e_out), f"replay {i}: top-k rows"
         want = topk_radix(g_logits.cpu().numpy(), g_mask.cpu().numpy(), case.context_lens.numpy(),
                           case.page_table_1().numpy(), step.width)
+        assert np.array_equal(g_out.cpu().numpy(), want), f"replay {i}: top-k rows differ from the oracle"
+
+
+P_ROWS, P_PREFIX, P_SLAB = 72, 5000, 24  # three 24-row slabs per replay
+
+
+def test_prefill_indexer_graph_replay(gpu):
+    """The prefill indexer (quant, then per slab: logits + top-2048) captured once and replayed
+    with new queries, weights and K of the same shapes: every replay bit-identical to an eager
+    run and to the oracle's selection (set and order)."""
+    cases = [wl.prefill_case(s, P_ROWS, P_PREFIX) for s in (51, 52, 53)]
+    n_keys = cases[0].n_keys
+    c0 = cases[0]
+    q = torch.zeros_like(c0.q, device=gpu)
+    w = torch.zeros_like(c0.w, device=gpu)
+    kv = torch.zeros_like(c0.kv, device=gpu)
+    bt = c0.block_table.to(gpu)  # one page order for every case: the kv contents change
+    lens = c0.lens.to(gpu)
+    out = torch.empty(P_ROWS, 2048, dtype=torch.int32, device=gpu)
+
+    def step():
+        q8, w8 = hcu_ops.quant_q_fp8(q, w)
+        return hcu_ops.prefill_indexer(q8, w8, kv, bt, lens, n_keys, max_slab_rows=P_SLAB, out=out), q8, w8
+
+    def load(case):
+        q.copy_(case.q)
+        w.copy_(case.w)
+        kv.copy_(case.kv)
+
+    load(cases[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_out, g_q8, g_w8 = step()
+    torch.cuda.synchronize()
+    slots = (c0.block_table.long()[torch.arange(n_keys) // 64] * 64 + torch.arange(n_keys) % 64).to(torch.int32)
+    for i, case in enumerate(cases[1:] + cases[:1]):
+        load(case)
+        e_out = step()[0].clone()  # eager run on the same inputs (writes `out` too)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out), f"replay {i}: top-k rows differ from the eager run"
+        lg = hcu_ops.mqa_logits_prefill(g_q8, g_w8, kv, bt, lens, n_keys)
+        want = topk_radix(lg.cpu().numpy(), None, case.lens.numpy(), slots[None, :].numpy(), n_keys,
+                          cu_seqlens_q=np.array([0, P_ROWS], dtype=np.int32))
         assert np.array_equal(g_out.cpu().numpy(), want), f"replay {i}: top-k rows differ from the oracle"
