@@ -193,6 +193,25 @@ __device__ void assign_cta(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* 
   }
 }
 
+// The same for up to 64 groups, computed by every wave on its own (lane g holds group g): no
+// LDS and no barrier before the CTA's first block-table read.  Returns {group (-1: none), index
+// within the group's CTAs, their count}, wave-uniform.
+__device__ __forceinline__ int3 assign_cta_wave(const DecodeArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int cta = blockIdx.x;
+  const bool in = lane < a.n_groups;
+  const int pages = in ? group_pages(a, lane) : 0;
+  const int incl_p = wave_prefix_sum(pages);
+  const int total = __builtin_amdgcn_readlane(incl_p, 63);
+  const int ctas = in ? group_ctas(pages, total, a.target) : 0;
+  const int incl = wave_prefix_sum(ctas);
+  const int c0 = incl - ctas;
+  const uint64_t m = __ballot(in && cta >= c0 && cta < incl);
+  if (m == 0) return make_int3(-1, 0, 0);
+  const int l = static_cast<int>(__builtin_ctzll(m));
+  return make_int3(l, cta - __builtin_amdgcn_readlane(c0, l), __builtin_amdgcn_readlane(ctas, l));
+}
+
 // Launch shape per (rows per CTA R, fused histogram): S page streams per CTA with NS LDS slots
 // each, and the block-table slice a CTA stages (the host keeps P / T within it; it also bounds a
 // row's tokens per CTA below 2^16 for the 16-bit histogram counters).  Measured on the 64-request
@@ -259,7 +278,19 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: row pointers become scalar
   const int cta = blockIdx.x;
 
-  assign_cta<NT>(a, s_w, s_assign);
+  int grp, jc, nj;
+  if (a.n_groups <= kWave) {  // block-uniform
+    const int3 as = assign_cta_wave(a);
+    grp = uniform(as.x);
+    jc = uniform(as.y);
+    nj = uniform(as.z);
+  } else {
+    assign_cta<NT>(a, s_w, s_assign);
+    __syncthreads();
+    grp = s_assign[0];
+    jc = s_assign[1];
+    nj = s_assign[2];
+  }
 
   // The paired top-k's per-row counters (words 0..2 of each row of the workspace's second
   // block [histograms rows*4096 | counters rows*4096 | counts rows*2]), a row per CTA; issued
@@ -269,14 +300,10 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     for (int64_t rr = cta; rr < a.batch; rr += gridDim.x)
       if (tid < 3) a.zero_ws[(a.batch + rr) * kBins + tid] = 0;
   };
-  __syncthreads();
-  const int grp = s_assign[0];
   if (grp < 0) {  // uniform: no pages for this CTA
     zero_share();
     return;
   }
-  const int jc = s_assign[1];
-  const int nj = s_assign[2];
 
   // wave = row r of the group x stream s: stream s takes the CTA's pages s, s + S, ...; its R
   // waves share each page through an LDS slot, one row each.

@@ -55,6 +55,19 @@ def test_decode_logits(gpu, heads, group, lens, rpc):
     _check_decode(case, lg, mask)
 
 
+@pytest.mark.parametrize("n_req,group", [(64, 1), (65, 1), (130, 1), (33, 2), (64, 2)])
+def test_decode_logits_group_counts(gpu, n_req, group):
+    """Up to 64 request groups every wave assigns its CTA's pages itself; past 64 the CTA does it
+    with block scans: both sides of the boundary, with empty and one-token rows among them."""
+    g = torch.Generator().manual_seed(n_req + group)
+    lens = torch.randint(1, 2600, (n_req,), generator=g)
+    lens[::7] = 0
+    lens[3::11] = 1
+    case = wl.decode_case(300 + n_req, lens.tolist(), group=group, heads=64, bt_pages=(2600 + group + 63) // 64 + 1)
+    _, _, lg, mask = _run_decode(case, gpu, rpc=group)
+    _check_decode(case, lg, mask)
+
+
 @pytest.mark.parametrize("pctas", [1, 3, 64, 1000])
 def test_decode_logits_cta_split(gpu, pctas):
     case = wl.decode_case(7, [9000, 4000], group=2, heads=64)
