@@ -607,6 +607,8 @@ int enqueue(DecodeArgs a, int heads, int R, int target_ctas, bool hist, const in
   }
   // Keep every CTA's page slice within the LDS block-table stage: P / T <= max_pages.
   const int64_t max_pages = n_groups * ((a.width + kPage - 1) / kPage);
+  DSA_REQUIRE(max_pages <= 0x7FFFFFFF, "%s: the groups' pages (%lld) must fit in 32 bits", who,
+              static_cast<long long>(max_pages));
   int64_t target = target_ctas;
   if (target * max_cta_pages < max_pages) target = (max_pages + max_cta_pages - 1) / max_cta_pages;
   const int64_t grid = target + n_groups;
