@@ -153,3 +153,56 @@ def test_topk_sampled_threshold_fallback(gpu, pattern):
     assert ret.data_ptr() == buf[1:].data_ptr()
     assert np.array_equal(np.asarray(buf[1:].cpu().numpy()), ref), f"{pattern} dense into out"
     assert (buf[0] == -7).all()
+
+
+def _crowded_row(g, L, m, need, kind):
+    """A row of L tokens whose threshold 12-bit digit (key[31:20]) holds exactly m members, of
+    which `need` are taken: 2048 - need tokens far above (>= 4.0), m members in [1.0, 1.125)
+    (low 20 key bits u: distinct, five values, one value, or one key[19:10] bucket), the rest
+    below 1.0; positions shuffled."""
+    if kind == "distinct":
+        u = torch.randperm(1 << 20, generator=g)[:m]
+    elif kind == "ties5":
+        u = torch.randperm(1 << 20, generator=g)[:5][torch.randint(0, 5, (m,), generator=g)]
+    elif kind == "equal":
+        u = torch.full((m,), 12345)
+    else:  # "bucket": one key[19:10] value, the order settled by key[9:0] alone
+        u = 777 * 1024 + torch.randint(0, 1024, (m,), generator=g)
+    members = (torch.full((m,), 0x3F800000, dtype=torch.int32) + u.to(torch.int32)).view(torch.float32)
+    above = 4.0 + torch.randperm(2048 - need, generator=g).float()
+    rest = torch.rand(L - (2048 - need) - m, generator=g) * 1.8 - 0.9
+    vals = torch.cat([above, members, rest])
+    return vals[torch.randperm(L, generator=g)]
+
+
+def test_topk_short_rows_crowded_threshold_digit(gpu):
+    """Rows of 2049..4096 tokens (resolved whole in one CTA on key[31:20]) whose threshold digit
+    holds 128, 129, 300, 512 or 513 members -- distinct keys, five keys, one key, or one
+    key[19:10] bucket -- with 1, half or all of them taken: the selection among the members (by
+    ranking, by two radix passes over key[19:0], or by the heavy-tie path past 512) matches the
+    oracle, set and order, for every implementation."""
+    g = torch.Generator().manual_seed(23)
+    W = 4160
+    rows = []
+    for m in [128, 129, 300, 512, 513]:
+        for need in [1, m // 2, m]:
+            for kind in ["distinct", "ties5", "equal", "bucket"]:
+                lo = 2048 - need + m
+                L = max(2049, int(torch.randint(lo, 4097, (1,), generator=g)))
+                rows.append((L, m, need, kind))
+    B = len(rows)
+    x = torch.full((B, W), 1e30)  # past a row's length: never read as a score
+    for b, (L, m, need, kind) in enumerate(rows):
+        x[b, :L] = _crowded_row(g, L, m, need, kind)
+    lengths = torch.tensor([r[0] for r in rows], dtype=torch.int32)
+    mask = torch.full((B, W // 16), -1, dtype=torch.int16)
+    pt = torch.arange(W, dtype=torch.int32)[None, :] + 3 + 100000 * torch.arange(B, dtype=torch.int32)[:, None]
+    ref = np.asarray(_oracle(x, mask, lengths, pt, W))
+    xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
+    for name, fn in IMPLS.items():
+        got = np.asarray(fn(xg, mg, lg, pg, cu).cpu().numpy())
+        bad = [rows[b] for b in range(B) if not np.array_equal(got[b], ref[b])]
+        assert not bad, f"impl={name}: rows (L, members, taken, keys) {bad[:4]}"
+    got = np.asarray(hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1).cpu().numpy())
+    assert np.array_equal(got, ref), "dense"
