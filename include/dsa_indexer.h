@@ -83,7 +83,8 @@ int dsa_quant_q_fp8(const uint16_t* q_bf16, const float* w, int64_t rows, int he
                     float* w_eff, hipStream_t stream);
 
 /* Indexer K-cache writer: quantises k (bf16 [n_tokens, 128]) per token with absmax/448 and
- * stores fp8 + fp32 scale at slots[i] in the 132-B paged layout. */
+ * stores fp8 + fp32 scale at slots[i] in the 132-B paged layout; a negative slot (a padded
+ * entry) stores nothing. */
 int dsa_store_k_cache(const uint16_t* k_bf16, int64_t n_tokens, const int32_t* slots,
                       uint8_t* kv_cache, int64_t page_stride_bytes, hipStream_t stream);
 

@@ -149,7 +149,8 @@ def quant_q_fp8(q, weights):
 
 
 def store_k_cache(k, slots, kv_cache):
-    """Quantises bf16 k [n, 128] per token and stores it at `slots` of the 132-B paged cache."""
+    """Quantises bf16 k [n, 128] per token and stores it at `slots` of the 132-B paged cache
+    (a negative slot, a padded entry, stores nothing)."""
     _C.store_k_cache(k, slots, kv_cache)
 
 

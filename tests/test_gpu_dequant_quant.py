@@ -104,3 +104,20 @@ def test_store_k_cache_bit_exact(gpu):
     kf = (k.view(torch.int16).numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
     ref = O.build_kv_cache(kf, slots.numpy(), n_pages)
     assert np.array_equal(kv_g.view(n_pages, -1).cpu().numpy(), ref)
+
+
+def test_store_k_cache_skips_padded_slots(gpu):
+    """Negative slots (padded entries) store nothing: the cache equals the oracle's cache of the
+    other entries alone, zero everywhere else."""
+    g = torch.Generator().manual_seed(5)
+    n_pages = 24
+    k = (torch.randn(1200, 128, generator=g) * 2).to(torch.bfloat16)
+    slots = torch.randperm(n_pages * 64, generator=g)[:1200].to(torch.int32)
+    slots[::7] = -1
+    slots[-1] = -5
+    kv_g = torch.zeros(n_pages, 64, 1, 132, dtype=torch.uint8, device=gpu)
+    hcu_ops.store_k_cache(k.to(gpu), slots.to(gpu), kv_g)
+    keep = (slots >= 0).numpy()
+    kf = (k.view(torch.int16).numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    ref = O.build_kv_cache(kf[keep], slots.numpy()[keep], n_pages)
+    assert np.array_equal(kv_g.view(n_pages, -1).cpu().numpy(), ref)
