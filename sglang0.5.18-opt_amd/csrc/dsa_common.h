@@ -58,17 +58,6 @@ __device__ __forceinline__ uint32_t fp8_e4m3_rne(float x) {
   return (nrm + sub - 8u) | sign;
 }
 
-// OCP fp8 e4m3fn -> fp32, exact (software; used where the throughput does not matter).
-__device__ __forceinline__ float fp8_e4m3_to_f32(uint32_t b) {
-  const uint32_t e = (b >> 3) & 0xFu;
-  const uint32_t m = b & 7u;
-  float v;
-  if (e == 0) v = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
-  else if (e == 15 && m == 7) v = __uint_as_float(0x7FC00000u);
-  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return (b & 0x80u) ? -v : v;
-}
-
 // Factors of the per-vector fp8 quantisation (hcu_ops/csrc/norm_quant.cu:13-14): for
 // amax = max|x| over the vector, the codes are fp8_e4m3_rne(x * inv) with inv = 448 / amax
 // (0 when amax == 0) and the dequantisation scale is amax / 448.
@@ -147,12 +136,6 @@ __device__ __forceinline__ int wave_prefix_sum(int x) {
   const int r2 = __builtin_amdgcn_readlane(x, 47);
   const int row = lane_id() >> 4;
   return x + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
 }
 
 // Exclusive prefix (lane order) and wave total of per-lane counts in [0, 7]: three ballots.
