@@ -991,7 +991,27 @@ __device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, con
     // A member is taken when its (key desc, token asc) rank is below need1; it is a tie when the
     // members with a key >= its own reach need1, i.e. its key is the threshold (the need1-th).
     // With exactly 2048 positive keys the reference's threshold is +0 and nothing is a tie.
-    if (tid < n_t1) {
+    const int m1 = __builtin_amdgcn_readfirstlane(n_t1);
+    if (m1 <= kWave) {  // block-uniform: wave 0 ranks up to 64 members from registers, each lane
+                        // against every other by readlane (9.5 -> 8.5 us for one 4096-token row)
+      if (tid < kWave) {
+        const uint32_t k = tid < m1 ? mk[tid] : 0u;
+        const int tk = tid < m1 ? mt[tid] : 0;
+        int rank = 0, ge = 0;
+        for (int j = 0; j < m1; ++j) {
+          const uint32_t kj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k), j));
+          const int tj = __builtin_amdgcn_readlane(tk, j);
+          rank += kj > k || (kj == k && tj < tk);
+          ge += kj >= k;
+        }
+        if (tid < m1) {
+          tok = tk;
+          val = mv[tid];
+          take = rank < need1;
+          tie = take && !plus0 && ge >= need1;
+        }
+      }
+    } else if (tid < n_t1) {
       const uint32_t k = mk[tid];
       tok = mt[tid];
       val = mv[tid];

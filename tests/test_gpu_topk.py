@@ -177,15 +177,15 @@ def _crowded_row(g, L, m, need, kind):
 
 def test_topk_short_rows_crowded_threshold_digit(gpu):
     """Rows of 2049..4096 tokens (resolved whole in one CTA on key[31:20]) whose threshold digit
-    holds 128, 129, 300, 512 or 513 members -- distinct keys, five keys, one key, or one
-    key[19:10] bucket -- with 1, half or all of them taken: the selection among the members (by
-    ranking, by two radix passes over key[19:0], or by the heavy-tie path past 512) matches the
-    oracle, set and order, for every implementation."""
+    holds 1 to 513 members -- distinct keys, five keys, one key, or one key[19:10] bucket -- with
+    1, half or all of them taken: the selection among the members (by register ranking up to 64,
+    pairwise LDS ranking up to 128, two radix passes over key[19:0] up to 512, the heavy-tie path
+    past it) matches the oracle, set and order, for every implementation."""
     g = torch.Generator().manual_seed(23)
     W = 4160
     rows = []
-    for m in [128, 129, 300, 512, 513]:
-        for need in [1, m // 2, m]:
+    for m in [1, 2, 63, 64, 65, 128, 129, 300, 512, 513]:
+        for need in sorted({1, max(1, m // 2), m}):
             for kind in ["distinct", "ties5", "equal", "bucket"]:
                 lo = 2048 - need + m
                 L = max(2049, int(torch.randint(lo, 4097, (1,), generator=g)))
