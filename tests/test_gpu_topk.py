@@ -175,14 +175,16 @@ def _crowded_row(g, L, m, need, kind):
     return vals[torch.randperm(L, generator=g)]
 
 
-def test_topk_short_rows_crowded_threshold_digit(gpu):
+@pytest.mark.parametrize("W", [4160, 4161, 40000, 40001])
+def test_topk_short_rows_crowded_threshold_digit(gpu, W):
     """Rows of 2049..4096 tokens (resolved whole in one CTA on key[31:20]) whose threshold digit
     holds 1 to 513 members -- distinct keys, five keys, one key, or one key[19:10] bucket -- with
     1, half or all of them taken: the selection among the members (by register ranking up to 64,
     pairwise LDS ranking up to 128, two radix passes over key[19:0] up to 512, the heavy-tie path
-    past it) matches the oracle, set and order, for every implementation."""
+    past it) matches the oracle, set and order, for every implementation.  Blocks 4160 / 4161
+    tokens wide take the one-CTA-per-row kernel, 40000 / 40001 the split kernel (its short-row
+    path, as for the short rows of a wide decode batch); the odd widths take the buffer loads."""
     g = torch.Generator().manual_seed(23)
-    W = 4160
     rows = []
     for m in [1, 2, 63, 64, 65, 128, 129, 300, 512, 513]:
         for need in sorted({1, max(1, m // 2), m}):
@@ -195,7 +197,7 @@ def test_topk_short_rows_crowded_threshold_digit(gpu):
     for b, (L, m, need, kind) in enumerate(rows):
         x[b, :L] = _crowded_row(g, L, m, need, kind)
     lengths = torch.tensor([r[0] for r in rows], dtype=torch.int32)
-    mask = torch.full((B, W // 16), -1, dtype=torch.int16)
+    mask = torch.full((B, (W + 15) // 16), -1, dtype=torch.int16)
     pt = torch.arange(W, dtype=torch.int32)[None, :] + 3 + 100000 * torch.arange(B, dtype=torch.int32)[:, None]
     ref = np.asarray(_oracle(x, mask, lengths, pt, W))
     xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
@@ -203,6 +205,6 @@ def test_topk_short_rows_crowded_threshold_digit(gpu):
     for name, fn in IMPLS.items():
         got = np.asarray(fn(xg, mg, lg, pg, cu).cpu().numpy())
         bad = [rows[b] for b in range(B) if not np.array_equal(got[b], ref[b])]
-        assert not bad, f"impl={name}: rows (L, members, taken, keys) {bad[:4]}"
+        assert not bad, f"W={W} impl={name}: rows (L, members, taken, keys) {bad[:4]}"
     got = np.asarray(hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1).cpu().numpy())
-    assert np.array_equal(got, ref), "dense"
+    assert np.array_equal(got, ref), f"W={W} dense"
