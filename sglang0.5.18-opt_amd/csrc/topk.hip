@@ -960,11 +960,11 @@ __device__ __forceinline__ bool resolve_cands(ResolveLds<NT, CAP>& L, int n, con
   bool take = false, tie = false;
   int tok = 0, val = 0;
   if (kShort && n_t1 > kRankDirect && !plus0) {  // block-uniform
-    // Many members of one plain 12-bit digit (a short row, resolved whole on key[31:20] = t1),
-    // at most one per thread: the threshold key by two 1024-bin passes over
-    // key[19:10] and key[9:0] in L.ck (free now) instead of ranking each member against all the
-    // others.  Every member at the threshold is flagged a tie and the tie count is the ties to
-    // take: the ordered emission gives them the last slots in token order and drops the rest.
+    // Many members of one plain 12-bit digit (a short row, resolved whole on key[31:20] = t1), at
+    // most one per thread: the threshold key by two 1024-bin passes over key[19:10] and key[9:0]
+    // in L.ck (free now) instead of ranking each member against all the others.  Every member at
+    // the threshold is flagged a tie and the tie count is the ties to take: the ordered emission
+    // gives them the last slots in token order and drops the rest.
     int* ha = reinterpret_cast<int*>(L.ck);
     int* hb = ha + 1024;
     zero_lds<NT>(ha, 2048);
