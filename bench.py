@@ -23,8 +23,10 @@ The JSON line also carries
 
 The default line (decode_mtp64, the quoted decode configuration, as `value`) also holds one object
 per other configuration -- prefill_8k_64k (the prefill headline), prefill_16k_128k, decode_32x16k,
-decode_1x4k -- and one for dequant_mla_393k (the 656-B MLA dequant), each with its own step time,
-roofline and CPU baseline.
+decode_1x4k -- and one each for dequant_k_74k (the 132-B indexer K dequant) and dequant_mla_393k
+(the 656-B MLA dequant), each with its own step time, roofline and CPU baseline.  Every workload
+also reports the median / min / max of 20 individually timed graph replays; a prefill step's
+time is that median (its roofline is taken over every slab's logits launch).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_mtp64]
 """
@@ -204,19 +206,27 @@ class PrefillStep:
                           memory_budget_bytes=self.slab * self.width * 4, max_slab_rows=self.slab, out=self.out)
         return self.out
 
-    def logits_only(self):
+    def slabs(self):
+        return [(r0, min(r0 + self.slab, self.case.rows)) for r0 in range(0, self.case.rows, self.slab)]
+
+    def logits_only(self, slab=None):
+        """The logits launches of every slab (slab=i: of slab i alone), q already quantised; each
+        slab's logits buffer is dropped before the next is made, as in the step."""
         if not hasattr(self, "_q8"):
             self._q8, self._w8 = self.h.quant_q_fp8(self.q, self.w)
-        r1 = self.slab
-        return self.h.mqa_logits_prefill(self._q8[:r1], self._w8[:r1], self.kv, self.bt, self.lens[:r1], self.width)
+        for i, (r0, r1) in enumerate(self.slabs()):
+            if slab is None or slab == i:
+                self.h.mqa_logits_prefill(self._q8[r0:r1], self._w8[r0:r1], self.kv, self.bt, self.lens[r0:r1],
+                                          self.width)
 
     def tokens(self):
         return self.case.tokens_scored()
 
-    def logits_flops(self):
-        """fp8 MFMA flops of one logits launch (the first slab): 2 * H * 128 per (row, key)."""
+    def logits_flops(self, slab=None):
+        """fp8 MFMA flops of the logits launches (every slab, or slab i): 2 * H * 128 per (row, key)."""
         H = self.case.q.shape[1]
-        return 2 * H * 128 * int(self.case.lens[:self.slab].long().sum())
+        rows = [(r0, r1) for i, (r0, r1) in enumerate(self.slabs()) if slab is None or slab == i]
+        return 2 * H * 128 * sum(int(self.case.lens[r0:r1].long().sum()) for r0, r1 in rows)
 
     def path_flops(self):
         H = self.case.q.shape[1]
@@ -277,20 +287,24 @@ class DequantStep:
         return self.case.tokens * self.tok_bytes
 
 
-def dequant_cpu_baseline(case, budget_s, tok_bytes):
-    """The oracle's numpy dequant over consecutive chunks of the slot list until budget_s."""
+def dequant_cpu_baseline(case, budget_s, tok_bytes, torch):
+    """The oracle's torch-CPU dequant (its numpy closed form restated on torch's intra-op threads)
+    over consecutive chunks of the slot list, repeated until budget_s."""
     from oracle import indexer as O
     mla = hasattr(case, "cache")
-    src = (case.cache.view(case.cache.shape[0], -1) if mla else case.kv.view(case.kv.shape[0], -1)).numpy()
-    slots = case.slots.numpy()
+    src = case.cache.view(case.cache.shape[0], -1) if mla else case.kv.view(case.kv.shape[0], -1)
+    slots = case.slots
+    threads, _ = cpu_threads(torch)
     done = 0
     t0 = time.perf_counter()
-    while done < slots.shape[0] and time.perf_counter() - t0 < budget_s:
-        s = slots[done:done + 8192]
-        O.dequant_mla(src, s) if mla else O.dequant_k_paged(src, s)
+    while time.perf_counter() - t0 < budget_s and (done < slots.shape[0] or time.perf_counter() - t0 < 1.0):
+        i = done % slots.shape[0]
+        s = slots[i:i + 65536]
+        O.cpu_dequant_torch(src, s, mla)
         done += s.shape[0]
     dt = time.perf_counter() - t0
-    return done * tok_bytes / dt / 1e9, f"{done} of {slots.shape[0]} tokens in {dt:.1f} s (numpy, one thread)"
+    return (done * tok_bytes / dt / 1e9, threads,
+            f"{done} tokens of the {slots.shape[0]}-slot list in {dt:.1f} s (torch CPU, {threads} threads)")
 
 
 # ---------------------------------------------------------------------------------------------
@@ -399,6 +413,22 @@ def cpu_threads(torch):
     return torch.get_num_threads(), avail
 
 
+def replay_stats(g, torch, per, n):
+    """n replays of step graph g (per steps each), each timed alone with HIP events on the current
+    stream: (median, min, max) ms per step."""
+    times = []
+    for _ in range(n):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) / per)
+    times.sort()
+    return times[len(times) // 2], times[0], times[-1]
+
+
 def timed_steps(step, args, torch):
     """ms per step: the step captured `steps_per_graph` to a hipGraph (as a serving loop captures the
     indexer inside its model step), replayed untimed for settle_ms, then W warm-up steps, then
@@ -422,7 +452,10 @@ def timed_steps(step, args, torch):
         g1.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / args.steps, per
+    med, lo, hi = replay_stats(g, torch, per, args.replays)
+    stats = {"replays": args.replays, "steps_per_replay": per, "median_ms_per_step": round(med, 5),
+             "min_ms_per_step": round(lo, 5), "max_ms_per_step": round(hi, 5)}
+    return start.elapsed_time(end) / args.steps, per, stats
 
 
 def run_indexer(name, args, torch, dev, steps=None):
@@ -437,10 +470,16 @@ def run_indexer(name, args, torch, dev, steps=None):
     torch.cuda.synchronize()
     if steps is not None:
         args = argparse.Namespace(**{**vars(args), **steps})
-    ms, per = timed_steps(step, args, torch)
+    ms, per, stats = timed_steps(step, args, torch)
+    timing = f"{args.steps} steps timed together between two synchronisations"
+    if not decode:
+        # a prefill step is milliseconds long: the median of the individually timed graph replays
+        # (hipEvents around each), with their spread beside it
+        ms = stats["median_ms_per_step"]
+        timing = f"median of {args.replays} individually timed hipGraph replays (hipEvents)"
     tokens = step.tokens()
     value = tokens / 1e3 / (ms / 1e3)
-    log(f"{name}: timed {args.steps} steps: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s")
+    log(f"{name}: {timing}: {ms * 1e3:.1f} us/step, {value:.4g} K-tokens/s (replays {stats})")
     if decode:
         # the launch as the step makes it: logits + the paired top-k's workspace prepared
         k_ms = kernel_time_ms(lambda: step.logits_only(hist=True), torch)
@@ -457,15 +496,23 @@ def run_indexer(name, args, torch, dev, steps=None):
         path = {"bound": "hbm", "achieved": round(pa, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(pa / HBM_PEAK_GBS, 4), "algorithmic_bytes": pb}
     else:
+        # every slab's logits launch (graphs of 20 passes over all slabs): flops over all of them
+        # against their summed duration, plus each slab alone
         k_ms = kernel_time_ms(step.logits_only, torch)
         kf = step.logits_flops()
         achieved = kf / (k_ms / 1e3) / 1e12
+        per_slab = []
+        for i in range(len(step.slabs())):
+            s_ms = kernel_time_ms(lambda i=i: step.logits_only(slab=i), torch, rounds=3, settle_ms=20.0)
+            per_slab.append({"kernel_us": round(s_ms * 1e3, 2),
+                             "frac": round(step.logits_flops(i) / (s_ms / 1e3) / 1e12 / FP8_PEAK_TFLOPS, 4)})
         # prefill runs the paged logits kernel with 8 query rows per CTA
         traffic, tsrc = profiled_traffic("mqa_logits_decode_kernel", name)
         roofline = {"bound": "mfma", "kernel": "mqa_logits_decode_kernel", "achieved": round(achieved, 1),
                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
                     "traffic": traffic, "traffic_source": tsrc, "algorithmic_flops": kf,
-                    "kernel_us": round(k_ms * 1e3, 2)}
+                    "launches": len(per_slab), "kernel_us": round(k_ms * 1e3, 2),
+                    "kernel_us_per_launch": round(k_ms * 1e3 / len(per_slab), 2), "slabs": per_slab}
         measured = mfma_ceiling(torch, dev)
         measured["logits_frac_of_mfma_only"] = round(achieved / measured["mfma_only"], 4)
         measured["logits_frac_of_mfma_with_epilogue_valu"] = round(achieved / measured["mfma_with_epilogue_valu"], 4)
@@ -487,9 +534,13 @@ def run_indexer(name, args, torch, dev, steps=None):
         log(f"{name}: cpu baseline {v:.4g} K-tokens/s on {threads} threads ({sample})")
     config = {"workload": f"{name}: {WORKLOADS[name]}", "query_rows": int(case.rows),
               "tokens_scored_per_step": int(tokens), "graph": f"hipGraph of {per} steps per replay",
-              "settle_ms": args.settle_ms}
+              "timing": timing, "settle_ms": args.settle_ms}
+    if not decode:
+        config["dequant"] = ("none in the step: the logits kernel reads the paged fp8 K directly, so the bf16 "
+                             "copy of K that the configuration names is never made (dequant_k_74k times that "
+                             "dequant on its own)")
     return {"value": round(value, 1), "ms_per_step": round(ms, 5), "steps": args.steps, "warmup": args.warmup,
-            "config": config, "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu}
+            "replays": stats, "config": config, "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu}
 
 
 def main(argv=None):
@@ -504,8 +555,10 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true",
                     help="the default decode_mtp64 line only (no objects for the other workloads)")
-    ap.add_argument("--no-dequant", action="store_true", help="no dequant_mla_393k object in the default line")
+    ap.add_argument("--no-dequant", action="store_true", help="no dequant objects (dequant_k_74k, dequant_mla_393k) in the default line")
     ap.add_argument("--steps-per-graph", type=int, default=10, help="steps captured in one hipGraph")
+    ap.add_argument("--replays", type=int, default=20,
+                    help="individually timed replays of the step graph (median / min / max reported)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB three times (the known-size kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE counters)")
@@ -533,7 +586,8 @@ def main(argv=None):
         line = {"metric": DEQUANT_METRIC, "value": d["value"], "unit": "GB/s", "n_gpus": 1, "steps": d["steps"],
                 "warmup": d["warmup"], "ms_per_step": d["ms_per_step"], "higher_is_better": True, "scaling": "weak",
                 "vs_baseline": None, "dtype": "fp8e4m3 -> bf16", "data": "synthetic (seeded, see tests/workloads.py)",
-                "config": d["config"], "roofline": d["roofline"], "cpu_baseline": d["cpu_baseline"]}
+                "replays": d["replays"], "config": d["config"], "roofline": d["roofline"],
+                "cpu_baseline": d["cpu_baseline"]}
         print(json.dumps(line), flush=True)
         return 0
 
@@ -542,18 +596,20 @@ def main(argv=None):
             "warmup": head["warmup"], "ms_per_step": head["ms_per_step"], "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 (fp32 accumulate)",
             "data": "synthetic (seeded, see tests/workloads.py)", "config": head["config"],
-            "roofline": head["roofline"], "path_roofline": head["path_roofline"], "cpu_baseline": head["cpu_baseline"]}
+            "replays": head["replays"], "roofline": head["roofline"], "path_roofline": head["path_roofline"],
+            "cpu_baseline": head["cpu_baseline"]}
     if args.workload == "decode_mtp64" and not args.no_prefill:
         # the second headline workload (the 64K-prefix chunked prefill) and the other configurations
         # in the same line, each with its own roofline and CPU baseline; prefill step counts sized
         # to about the same wall time
-        few = {"steps": max(2, args.steps // 10), "warmup": max(1, args.warmup // 10), "steps_per_graph": 1}
+        few = {"steps": max(2, args.steps // 10), "warmup": max(1, args.warmup // 10), "steps_per_graph": 1,
+               "replays": max(20, args.replays)}
         for name, steps in (("prefill_8k_64k", few), ("prefill_16k_128k", few), ("decode_32x16k", None),
                             ("decode_1x4k", None)):
             line[name] = {"metric": METRIC, "unit": "K-tokens/s", **run_indexer(name, args, torch, dev, steps=steps)}
         if not args.no_dequant:
-            line["dequant_mla_393k"] = {"metric": DEQUANT_METRIC, "unit": "GB/s",
-                                        **run_dequant("dequant_mla_393k", args, torch, dev)}
+            for name in ("dequant_k_74k", "dequant_mla_393k"):
+                line[name] = {"metric": DEQUANT_METRIC, "unit": "GB/s", **run_dequant(name, args, torch, dev)}
     print(json.dumps(line), flush=True)
     return 0
 
@@ -566,7 +622,7 @@ def run_dequant(name, args, torch, dev):
     log(f"built {name} inputs on the CPU in {time.perf_counter() - t0:.1f} s")
     step = DequantStep(case, dev)
     torch.cuda.synchronize()
-    ms, per = timed_steps(step, args, torch)
+    ms, per, stats = timed_steps(step, args, torch)
     nb = step.bytes()
     value = nb / (ms / 1e3) / 1e9
     k_ms = kernel_time_ms(step, torch)
@@ -578,10 +634,12 @@ def run_dequant(name, args, torch, dev):
                 "algorithmic_bytes": nb, "kernel_us": round(k_ms * 1e3, 2)}
     cpu = None
     if not args.no_cpu_baseline:
-        v, sample = dequant_cpu_baseline(case, args.cpu_budget, step.tok_bytes)
-        cpu = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port", "sample": sample, "cpu": cpu_model()}
+        v, threads, sample = dequant_cpu_baseline(case, min(args.cpu_budget, 5.0), step.tok_bytes, torch)
+        cpu = {"value": round(v, 3), "unit": "GB/s", "cores": threads, "kind": "port", "sample": sample,
+               "cpu": cpu_model()}
         log(f"cpu baseline {v:.3g} GB/s ({sample})")
     return {"value": round(value, 1), "ms_per_step": round(ms, 5), "steps": args.steps, "warmup": args.warmup,
+            "replays": stats,
             "config": {"workload": f"{name}: {WORKLOADS[name]}", "tokens": int(case.tokens),
                        "bytes_per_token": step.tok_bytes, "graph": f"hipGraph of {per} launches per replay",
                        "settle_ms": args.settle_ms},

@@ -70,6 +70,28 @@ def dequant_mla(cache, slots):
     return out
 
 
+def cpu_dequant_torch(src, slots, mla):
+    """torch-CPU restatement of dequant_k_paged (mla=False: src u8 [pages, 8448] of the 132-B
+    layout) and dequant_mla (mla=True: src u8 [pool, 656]) for valid slots, on torch's intra-op
+    threads (the multi-thread CPU baseline): bf16 [n, 128] / [n, 576].  fp8 -> f32 is exact, the
+    product one f32 rounding, .to(bfloat16) round-to-nearest-even, as in the numpy forms above."""
+    import torch
+    slots = slots.long()
+    if mla:
+        rows = src[slots]
+        n = rows.shape[0]
+        vals = rows[:, :512].contiguous().view(torch.float8_e4m3fn).float().view(n, 4, 128)
+        scale = rows[:, 512:528].contiguous().view(torch.float32).view(n, 4, 1)
+        nope = (vals * scale).view(n, 512).to(torch.bfloat16)
+        rope = rows[:, 528:656].contiguous().view(torch.bfloat16)
+        return torch.cat([nope, rope], 1)
+    page, off = slots // PAGE, slots % PAGE
+    cols = off[:, None] * HEAD_DIM + torch.arange(HEAD_DIM)[None, :]
+    codes = src[page[:, None], cols]
+    sc = src[page[:, None], PAGE_FP8 + off[:, None] * 4 + torch.arange(4)[None, :]].contiguous().view(torch.float32)
+    return (codes.view(torch.float8_e4m3fn).float() * sc).to(torch.bfloat16)
+
+
 # --------------------------------------------------------------------------------------------
 # Per-vector fp8 quantisation (hcu_ops/csrc/norm_quant.cu:13-14: amax = max|x| taken with fmaxf
 # from 0, so NaN elements do not count, scale = amax / 448, q = fp8(x * (448 / amax)),

@@ -84,6 +84,24 @@ def test_dequant_mla_matches_torch_closed_form():
     assert (got2[~keep] == 0).all() and np.array_equal(got2[keep], got[keep])
 
 
+def test_cpu_dequant_torch_matches_numpy_oracle():
+    """The torch-CPU dequant of the multi-thread CPU baseline gives the numpy oracle's bits (both
+    layouts), so the baseline times the same computation."""
+    case = wl.decode_case(12, [700, 300], group=1, heads=32)
+    kv = _kv_np(case)
+    slots = torch.randperm(kv.shape[0] * 64, generator=torch.Generator().manual_seed(3))[:900]
+    got = O.cpu_dequant_torch(torch.from_numpy(kv), slots, mla=False).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, O.dequant_k_paged(kv, slots.numpy()))
+    g = torch.Generator().manual_seed(4)
+    pool = 50
+    cache = (torch.randn(pool, 656, generator=g) * 0.1).to(torch.float8_e4m3fn).view(torch.uint8)
+    cache[:, 512:528] = (torch.rand(pool, 4, generator=g) * 0.02 + 1e-3).view(torch.uint8)
+    cache[:, 528:] = torch.randn(pool, 64, generator=g).to(torch.bfloat16).view(torch.uint8)
+    slots = torch.randint(0, pool, (300,), generator=g)
+    got = O.cpu_dequant_torch(cache, slots, mla=True).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, O.dequant_mla(cache.numpy(), slots.numpy()))
+
+
 def test_quant_vectors_matches_torch_generator():
     g = torch.Generator().manual_seed(9)
     x = torch.cat([torch.randn(5000, 128, generator=g) * 3, torch.zeros(2, 128),
