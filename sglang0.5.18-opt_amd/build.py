@@ -6,7 +6,9 @@
 Usage: python build.py [--jobs N] [--no-bind]
 """
 import argparse
+import json
 import os
+import re
 import subprocess
 import sys
 import sysconfig
@@ -37,6 +39,23 @@ def _run(cmd):
     return out
 
 
+def kernel_resources(remarks):
+    """{kernel: {field: value}} from hipcc's -Rpass-analysis=kernel-resource-usage remarks (VGPRs,
+    AGPRs, scratch bytes per lane, LDS bytes per block, occupancy in waves per SIMD)."""
+    fields = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch",
+              "LDS Size [bytes/block]": "lds", "Occupancy [waves/SIMD]": "occupancy"}
+    res, cur = {}, None
+    for line in remarks.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = res.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+(.+?): (\d+)\s*\[", line)
+        if cur is not None and m and m.group(1) in fields:
+            cur[fields[m.group(1)]] = int(m.group(2))
+    return res
+
+
 def build_library(jobs):
     os.makedirs(OBJ, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
@@ -44,11 +63,19 @@ def build_library(jobs):
 
     def compile_one(src):
         obj = os.path.join(OBJ, src.rsplit(".", 1)[0] + ".o")
-        _run([hipcc, *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj])
-        return obj
+        out = _run([hipcc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-x", "hip", "-c",
+                    os.path.join(CSRC, src), "-o", obj])
+        return obj, kernel_resources(out)
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(compile_one, HIP_SOURCES))
+        built = list(ex.map(compile_one, HIP_SOURCES))
+    objs = [o for o, _ in built]
+    usage = {}
+    for _, r in built:
+        usage.update(r)
+    # per-kernel register / scratch / LDS use of this build (tests/test_build_resources.py reads it)
+    with open(os.path.join(OBJ, "kernel_resources.json"), "w") as f:
+        json.dump(usage, f, indent=1, sort_keys=True)
     lib = os.path.join(PKG, "libdsa_indexer.so")
     tmp = lib + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp, "-Wl,-soname,libdsa_indexer.so"])
