@@ -118,6 +118,7 @@ struct DecodeArgs {
   int32_t* zero_ws;   // non-null: the paired top-k's workspace, whose counters are zeroed here
   int64_t batch;
   int nt_logits;      // logits stored nontemporally (a logits block larger than the L2s hold)
+  int slice_pages;    // > 0: slice-major assignment (assign_slices) with slices of this many pages
 };
 
 __device__ __forceinline__ int clamp_len(int l, int width) { return l < 0 ? 0 : (l > width ? width : l); }
@@ -190,6 +191,60 @@ __device__ void assign_cta(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* 
       }
       c0 += n;
     }
+  }
+}
+
+// Slice-major assignment (the prefill launches): the K pages of every group are cut into slices of
+// SL = a.slice_pages pages, and CTA c takes the c-th (slice, group) pair in slice-then-group
+// order, so the CTAs resident at one time -- consecutive blockIdx, spread over the 8 XCDs by
+// blockIdx % 8 -- work on the same slice of K for different row groups: each XCD's L2 then holds
+// one slice (SL * 8448 B) that all of its CTAs read, where the group-major balanced grid has every
+// XCD's resident CTAs spread over the whole K range (a prefill's 10-20 MB of K misses the L2s).
+// s_assign = {group (-1: none), slice, the group's pages}.  Ends before a barrier (the caller's).
+constexpr int kMaxSlices = 64;  // slices a group may have (the host sizes SL for it)
+
+template <int NT>
+__device__ void assign_slices(const DecodeArgs& a, int (&s_w)[2][NT / kWave], int* s_nsl, int* s_assign) {
+  const int tid = threadIdx.x;
+  const int cta = blockIdx.x;
+  const int SL = a.slice_pages;
+  // s_nsl[n] = groups with n slices
+  for (int i = tid; i <= kMaxSlices; i += NT) s_nsl[i] = 0;
+  if (tid == 0) s_assign[0] = -1;
+  __syncthreads();
+  for (int g = tid; g < a.n_groups; g += NT) {
+    const int ns = (group_pages(a, g) + SL - 1) / SL;
+    atomicAdd(&s_nsl[ns < kMaxSlices ? ns : kMaxSlices], 1);
+  }
+  __syncthreads();
+  // this CTA's slice j: pairs of slice j are the groups with more than j slices
+  int j = 0, before = 0, in_j = 0;
+  for (; j < kMaxSlices; ++j) {
+    in_j = 0;
+    for (int n = j + 1; n <= kMaxSlices; ++n) in_j += s_nsl[n];
+    if (cta < before + in_j) break;
+    before += in_j;
+  }
+  if (j == kMaxSlices) return;  // block-uniform: no pair left for this CTA
+  const int rank = cta - before;  // the rank-th group (in group order) with more than j slices
+  int seen = 0;
+  for (int g0 = 0; g0 < a.n_groups; g0 += NT) {  // block-uniform
+    const int g = g0 + tid;
+    int pages = 0;
+    bool has = false;
+    if (g < a.n_groups) {
+      pages = group_pages(a, g);
+      has = (pages + SL - 1) / SL > j;
+    }
+    int total;
+    const int pre = block_excl_sum<NT>(has ? 1 : 0, total, s_w[(g0 / NT) & 1]);
+    if (has && seen + pre == rank) {
+      s_assign[0] = g;
+      s_assign[1] = j;
+      s_assign[2] = pages;
+    }
+    seen += total;
+    if (seen > rank) break;  // block-uniform
   }
 }
 
@@ -271,6 +326,7 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   __shared__ int s_cnt[2 * R];
   __shared__ int s_w[2][NT / kWave];
   __shared__ int s_assign[3];  // group, index within the group's CTAs, the group's CTA count
+  __shared__ int s_nsl[kMask ? 1 : kMaxSlices + 1];  // slice-major assignment (prefill, no mask)
   __shared__ int s_bt[Sh::kMaxPages];
 
   const int tid = threadIdx.x;
@@ -279,7 +335,18 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
   const int cta = blockIdx.x;
 
   int grp, jc, nj;
-  if (a.n_groups <= kWave) {  // block-uniform
+  int slice_begin = -1, slice_pages = 0;  // slice-major: the CTA's first page, its group's pages
+  if (!kMask && a.slice_pages > 0) {  // block-uniform
+    if constexpr (!kMask) {
+      assign_slices<NT>(a, s_w, s_nsl, s_assign);
+      __syncthreads();
+      grp = s_assign[0];
+      jc = s_assign[1];
+      nj = 1;
+      slice_begin = jc * a.slice_pages;
+      slice_pages = s_assign[2];
+    }
+  } else if (a.n_groups <= kWave) {  // block-uniform
     const int3 as = assign_cta_wave(a);
     grp = uniform(as.x);
     jc = uniform(as.y);
@@ -323,8 +390,9 @@ __global__ __launch_bounds__((Shape<R, kHist>::kThreads)) __attribute__((amdgpu_
     hlim = h > kTopK ? h : 0;
   }
   const int pages = (max_len + kPage - 1) / kPage;
-  const int p_begin = static_cast<int>(static_cast<int64_t>(pages) * jc / nj);
-  const int p_end = static_cast<int>(static_cast<int64_t>(pages) * (jc + 1) / nj);
+  const int p_begin = slice_begin >= 0 ? slice_begin : static_cast<int>(static_cast<int64_t>(pages) * jc / nj);
+  const int p_end = slice_begin >= 0 ? min(slice_begin + a.slice_pages, slice_pages)
+                                     : static_cast<int>(static_cast<int64_t>(pages) * (jc + 1) / nj);
   const int n_local = p_end - p_begin;  // <= Sh::kMaxPages by the host's choice of target
   const int32_t* btr = a.bt + static_cast<int64_t>(group_row) * a.bt_stride + p_begin;
 
@@ -603,11 +671,33 @@ void shape_host(int R, bool hist, int& ctas_per_cu, int& max_pages) {
 // Enqueues the kernel for a.batch rows in groups of R (a.group rows share a block-table row;
 // a.width caps the lengths).  a's pointers, strides and sizes are set and checked by the caller.
 int enqueue(DecodeArgs a, int heads, int R, int target_ctas, bool hist, const int32_t* hist_lens, int32_t* hist_ws,
-            hipStream_t stream, const char* who) {
+            hipStream_t stream, const char* who, bool slice_major = false) {
   const int64_t n_groups = a.batch / R;
   DSA_REQUIRE(n_groups <= 0x3FFFFFFF, "%s: too many rows", who);
   int ctas_per_cu = 1, max_cta_pages = 1;
   shape_host(R, hist, ctas_per_cu, max_cta_pages);
+  a.slice_pages = 0;
+  const int64_t width_pages = (a.width + kPage - 1) / kPage;
+  // (the maskless eight-row instantiation is the one that carries the slice-major assignment)
+  if (slice_major && R == 8 && a.mask == nullptr && width_pages <= static_cast<int64_t>(kMaxSlices) * max_cta_pages) {
+    // slices as long as the block-table stage allows (the balanced grid's slice length at these
+    // shapes), a CTA per (slice, group) pair the widest group could need
+    const int64_t n_sl = (width_pages + max_cta_pages - 1) / max_cta_pages;
+    const int64_t grid = n_groups * n_sl;
+    DSA_REQUIRE(grid <= 0x7FFFFFFF, "%s: grid too large", who);
+    a.R = R;
+    a.n_groups = static_cast<int>(n_groups);
+    a.slice_pages = static_cast<int>((width_pages + n_sl - 1) / n_sl);
+    a.nt_logits = a.batch * static_cast<int64_t>(a.width) * 4 > (16ll << 20) ? 1 : 0;
+    a.target = 0;
+    a.hist_lens = nullptr;
+    a.hist_ws = nullptr;
+    a.zero_ws = nullptr;
+    const uint32_t g = static_cast<uint32_t>(grid);
+    if (heads == 64) launch_r<64, false>(a, R, g, stream);
+    else launch_r<32, false>(a, R, g, stream);
+    return check_launch(who);
+  }
   if (target_ctas <= 0) {
     // All CTAs resident at once: the per-group rounding adds up to one CTA per group, so aim
     // below the resident count by the group count.
@@ -746,7 +836,7 @@ extern "C" int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int hea
     a.mask_stride = 0;
     a.group = static_cast<int>(n);
     a.batch = n;
-    const int st = enqueue(a, heads, R, 0, false, nullptr, nullptr, stream, "dsa_mqa_logits_prefill");
+    const int st = enqueue(a, heads, R, 0, false, nullptr, nullptr, stream, "dsa_mqa_logits_prefill", true);
     if (st != DSA_OK) return st;
     done += n;
   }
