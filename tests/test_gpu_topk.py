@@ -46,6 +46,21 @@ def test_topk_distributions(gpu, dist, B):
                 assert np.array_equal(got, ref), f"{dist} B={B} L={L} ragged={ragged} impl={name}"
 
 
+@pytest.mark.parametrize("dist", wl.TOPK_DISTS)
+def test_topk_one_cta_rows_to_16k(gpu, dist):
+    """One CTA per row (widths up to 32K never split) at 16,384 tokens wide, one short of it
+    (unaligned: scalar loads) and a middle width; full and ragged rows."""
+    for W in [16384, 16383, 9000]:
+        for ragged in [False, True]:
+            L = W if not ragged else W - 5
+            x, mask, lengths, pt = wl.topk_scores(24, L, dist, W=W, ragged=ragged, seed=W + ragged)
+            ref = np.asarray(_oracle(x, mask, lengths, pt, W))
+            xg, mg, lg, pg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu)
+            cu = torch.arange(25, dtype=torch.int32, device=gpu)
+            got = np.asarray(IMPLS["single"](xg, mg, lg, pg, cu).cpu().numpy())
+            assert np.array_equal(got, ref), f"{dist} W={W} ragged={ragged}"
+
+
 @pytest.mark.parametrize("dist", ["relu_sum", "narrow", "sparse2"])
 def test_topk_production_width(gpu, dist):
     """Score width = page-table capacity (1M) with ragged rows of 16K..128K tokens."""
