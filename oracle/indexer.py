@@ -140,22 +140,28 @@ def head_scores(q8_codes_row, k8_codes):
 
 
 def logits_row(q8_codes_row, w_row, k8_codes, k_scale):
-    """(logit float64 [n], abs-magnitude float64 [n]) of one query row over keys.
+    """(logit, magnitude, dot magnitude), float64 [n] each, of one query row over keys.
     The magnitude A_t = scale_t * sum_h |w_h| relu(acc_h) bounds |logit| and sets the scale of
-    the fp32 rounding error (it equals |logit| when all weights share a sign)."""
+    the fp32 rounding error (it equals |logit| when all weights share a sign).  The dot magnitude
+    M_t = scale_t * sum_h |w_h| sum_d |q8_hd k8_td| (every head, every product) sets the scale of
+    a matrix instruction's accumulation error, which is relative to the products it sums."""
     acc = head_scores(q8_codes_row, k8_codes)
     r = np.maximum(acc, 0.0)
     w = np.asarray(w_row, dtype=np.float64)
     s = np.asarray(k_scale, dtype=np.float64)
-    return (w @ r) * s, (np.abs(w) @ r) * s
+    q = np.abs(fp8_decode(q8_codes_row).astype(np.float64))
+    k = np.abs(fp8_decode(k8_codes).astype(np.float64))
+    return (w @ r) * s, (np.abs(w) @ r) * s, (np.abs(w) @ (q @ k.T)) * s
 
 
 def mqa_logits_decode(q8, w, kv, context_lens, block_table, group, width):
     """Oracle of dsa_mqa_logits_decode: (logits float64 [B, width] with NaN where not
-    written, magnitude float64 [B, width], mask int16 [B, width / 16])."""
+    written, magnitude and dot magnitude float64 [B, width] (logits_row), mask int16
+    [B, width / 16])."""
     B = q8.shape[0]
     logits = np.full((B, width), np.nan)
     mag = np.zeros((B, width))
+    dmag = np.zeros((B, width))
     bits = np.zeros((B, width), dtype=bool)
     lens = np.clip(np.asarray(context_lens, dtype=np.int64), 0, width)
     for g0 in range(0, B, group):
@@ -168,11 +174,12 @@ def mqa_logits_decode(q8, w, kv, context_lens, block_table, group, width):
             L = int(lens[r])
             if L == 0:
                 continue
-            lg, mg = logits_row(q8[r], w[r], codes[:L], scale[:L])
+            lg, mg, dm = logits_row(q8[r], w[r], codes[:L], scale[:L])
             logits[r, :L] = lg
             mag[r, :L] = mg
+            dmag[r, :L] = dm
             bits[r, :L] = lg != 0.0
-    return logits, mag, pack_mask(bits)
+    return logits, mag, dmag, pack_mask(bits)
 
 
 def pack_mask(bits):
@@ -193,18 +200,21 @@ def unpack_mask(mask, width):
 
 
 def mqa_logits_prefill(q8, w, kv, block_table, lens, width):
-    """Oracle of dsa_mqa_logits_prefill: rows of one request, key t < lens[r]."""
+    """Oracle of dsa_mqa_logits_prefill: rows of one request, key t < lens[r]: (logits,
+    magnitude, dot magnitude) as mqa_logits_decode."""
     rows = q8.shape[0]
     n = int(np.clip(np.max(lens), 0, width)) if rows else 0
     codes, scale = kv_tokens(kv, slots_of(block_table, n))
     logits = np.full((rows, width), np.nan)
     mag = np.zeros((rows, width))
+    dmag = np.zeros((rows, width))
     for r in range(rows):
         L = int(np.clip(lens[r], 0, width))
-        lg, mg = logits_row(q8[r], w[r], codes[:L], scale[:L])
+        lg, mg, dm = logits_row(q8[r], w[r], codes[:L], scale[:L])
         logits[r, :L] = lg
         mag[r, :L] = mg
-    return logits, mag
+        dmag[r, :L] = dm
+    return logits, mag, dmag
 
 
 # --------------------------------------------------------------------------------------------

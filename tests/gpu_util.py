@@ -5,13 +5,17 @@ import torch
 from oracle import indexer as O
 from oracle.fp8 import fp8_decode
 
-# Logits tolerance (fp32 accumulation on fp8 MFMA vs the exact fp64 oracle):
+# Logits tolerance (fp8 MFMA + fp32 epilogue vs the exact fp64 oracle):
 #  (a) every token: |gpu - oracle| <= RTOL * A_t, where A_t = s_t * sum_h |w_h| relu(acc_h) is the
 #      magnitude of the weighted ReLU sum (A_t = |logit| when the head weights share a sign);
-#  (b) tokens whose logit is not cancelled by more than CANCEL across heads (|logit| >= A_t /
-#      CANCEL): the plain relative bound |gpu - oracle| <= RTOL * |oracle|.
-# Near-total cancellation (|logit| << A_t) amplifies any fp32 rounding, an fp32 reference's own
-# included, so (b) excludes it and (a) bounds it.
+#  (b) tokens whose logit is cancelled by at most CANCEL, across heads (|logit| >= A_t / CANCEL)
+#      and inside the dot products (|logit| >= M_t / CANCEL, M_t = s_t sum_h |w_h| sum_d
+#      |q8_hd k8_td|): the plain relative bound |gpu - oracle| <= RTOL * |oracle|.
+# One v_mfma_f32_16x16x128_f8f6f4 is not an fp32 sum of its 128 exact products: measured on
+# gfx950 its result is off by up to 1.5e-5 (normal keys) and 5.0e-5 (Student-t(4) keys) of the
+# summed |products| (a sequential fp32 sum: 5e-8), so a logit whose dot products cancel carries
+# that error relative to M_t, not to |logit|; (b) leaves such tokens to (a), as it leaves the
+# ones whose heads cancel.
 RTOL = 1e-3
 CANCEL = 20.0
 
@@ -24,14 +28,15 @@ def q_bits(q_bf16):
     return q_bf16.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def check_logits(got, ref, mag, what=""):
-    """Asserts the tolerance above; returns (max err / A_t, max relative err over (b))."""
+def check_logits(got, ref, mag, dmag, what=""):
+    """Asserts the tolerance above (mag = A_t, dmag = M_t); returns (max err / A_t, max relative
+    err over (b))."""
     got = np.asarray(got, dtype=np.float64)
     err = np.abs(got - ref)
     bad = err > RTOL * mag + 1e-30
     worst_mag = float((err / np.maximum(mag, 1e-30)).max()) if err.size else 0.0
     assert not bad.any(), f"{what}: {int(bad.sum())} logits outside {RTOL} * magnitude; worst {worst_mag:.3e}"
-    plain = (np.abs(ref) >= mag / CANCEL) & (mag > 0)  # exact zeros are covered by (a)
+    plain = (np.abs(ref) >= np.maximum(mag, dmag) / CANCEL) & (mag > 0)  # exact zeros are covered by (a)
     rel = err[plain] / np.abs(ref[plain]) if plain.any() else np.zeros(1)
     worst_rel = float(rel.max())
     assert worst_rel <= RTOL, f"{what}: relative error {worst_rel:.3e} > {RTOL} on an uncancelled logit"

@@ -13,8 +13,11 @@ Prefill (prefill_8k_64k, prefill_16k_128k with Student-t K): quant_q_fp8 -> pref
 4096-row slabs.  Every row of every slab equals an exact selection computed by torch on the GPU
 from the same logits (int64 composite keys (key << 21) | (2^21 - 1 - token), i.e. key
 descending, token ascending), put in the reference's order.  About 32 rows spread over the
-slabs (the first and last row of each slab among them): q8 / weights bit-exact, logits against the fp64 oracle, and the
-top-k row equal to the oracle's C radix select."""
+slabs (the first and last row of each slab among them): logits against the CPU fp64 oracle
+(indexer.logits_row) and the top-k row equal to the oracle's C radix select.  Every row: q8 /
+weights bit-exact against the oracle, and every logit within the tolerance against the same
+fp64 closed form evaluated on the GPU (chunks of rows, one fp64 matmul per chunk), itself checked
+against indexer.logits_row on the sampled rows."""
 import numpy as np
 import pytest
 import torch
@@ -53,20 +56,58 @@ def test_decode_config_full_size(gpu, name):
     rq8, rw = oracle_q(case)
     assert np.array_equal(q8.view(torch.uint8).cpu().numpy(), rq8), "q8 differs from the oracle"
     assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32)), "folded weights differ"
-    ref, mag, ref_mask = oracle_decode(case, rq8, rw)
+    ref, mag, dmag, ref_mask = oracle_decode(case, rq8, rw)
     got_mask = mask.cpu().numpy()
     assert np.array_equal(got_mask, ref_mask), "nonzero mask differs from the oracle"
     got = logits.cpu().numpy()
     worst = 0.0
     for r in range(case.rows):
         L = int(case.context_lens[r])
-        wm, _ = check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"{name} row {r}")
+        wm, _ = check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"{name} row {r}")
         worst = max(worst, wm)
     want = topk_radix(got, got_mask, case.context_lens.numpy(), pt.numpy(), case.width)
     sel = out.cpu().numpy()
     bad = [r for r in range(case.rows) if not np.array_equal(sel[r], want[r])]
     assert not bad, f"{name}: top-k rows {bad[:8]} differ from the oracle's selection"
     _log(f"{name}: {case.rows} rows match; worst logit error / magnitude {worst:.2e}")
+
+
+def _ref_logits_gpu(q8, w, k8, kscale, lens):
+    """fp64 (logits, magnitude, dot magnitude) [rows, width] of indexer.logits_row on the GPU:
+    q8 [rows, H, 128] and k8 [width, 128] fp8 codes decoded exactly, acc = q8 . k8 per head, then
+    scale_t * sum_h w_h relu(acc), scale_t * sum_h |w_h| relu(acc) and scale_t * sum_h |w_h|
+    |q8| . |k8|; NaN at t >= lens[r]."""
+    rows, H, D = q8.shape
+    qd = q8.view(torch.float8_e4m3fn).to(torch.float64).reshape(rows * H, D)
+    acc = torch.matmul(qd, k8).view(rows, H, -1).clamp_min_(0.0)  # k8: [128, width] fp64, contiguous
+    wd = w.to(torch.float64).unsqueeze(1).contiguous()  # [rows, 1, H] @ [rows, H, width]
+    wa = wd.abs().contiguous()
+    lg = torch.bmm(wd, acc).squeeze(1) * kscale[None, :]
+    mag = torch.bmm(wa, acc).squeeze(1) * kscale[None, :]
+    del acc
+    dots = torch.matmul(qd.abs(), k8.abs()).view(rows, H, -1)
+    dmag = torch.bmm(wa, dots).squeeze(1) * kscale[None, :]
+    del dots
+    t = torch.arange(lg.shape[1], device=lg.device)
+    out = t[None, :] >= lens.long()[:, None]
+    nan = float("nan")
+    return lg.masked_fill_(out, nan), mag.masked_fill_(out, nan), dmag.masked_fill_(out, nan)
+
+
+def _check_logits_gpu(got, ref, mag, dmag, what):
+    """check_logits on the GPU over the finite reference entries: |got - ref| <= RTOL * magnitude,
+    and the relative error <= RTOL where the logit is not cancelled (|ref| >= max(magnitude, dot
+    magnitude) / CANCEL)."""
+    from gpu_util import CANCEL, RTOL
+    ok = ~torch.isnan(ref)
+    err = (got.to(torch.float64) - ref).abs()
+    bad = ok & (err > RTOL * mag + 1e-30)
+    assert not bool(bad.any()), f"{what}: {int(bad.sum())} logits outside {RTOL} * magnitude"
+    plain = ok & (ref.abs() >= torch.maximum(mag, dmag) / CANCEL) & (mag > 0)
+    rel = torch.where(plain, err / ref.abs().clamp_min(1e-300), torch.zeros_like(err))
+    worst = float(rel.max()) if rel.numel() else 0.0
+    assert worst <= RTOL, f"{what}: relative error {worst:.3e} > {RTOL} on an uncancelled logit"
+    return float(torch.where(ok, err / mag.clamp_min(1e-30), torch.zeros_like(err)).max())
 
 
 def _exact_topk_torch(lg, lens, pt):
@@ -122,6 +163,17 @@ def test_prefill_config_full_size(gpu, name):
                                   max_slab_rows=SLAB)
     torch.cuda.synchronize()
 
+    # q8 / weights of every row against the oracle; the keys as fp64 for the GPU restatement
+    rq8_all, rw_all = O.quant_q(q_bits(case.q), case.w.numpy())
+    assert np.array_equal(q8.view(torch.uint8).cpu().numpy(), rq8_all), "q8 differs from the oracle"
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw_all.view(np.uint32)), "folded weights differ"
+    del rq8_all, rw_all
+    codes, scale = O.kv_tokens(kv_np(case.kv), O.slots_of(case.block_table.numpy(), width))
+    k8 = torch.from_numpy(np.ascontiguousarray(codes)).to(gpu).view(torch.float8_e4m3fn).to(torch.float64)
+    k8 = k8.t().contiguous()
+    ks = torch.from_numpy(scale).to(gpu).to(torch.float64)
+    chunk = 8
+
     n_slabs = (rows + SLAB - 1) // SLAB
     picks = set(np.linspace(0, rows - 1, 32 - 2 * n_slabs).astype(int).tolist())
     for s in range(n_slabs):
@@ -137,20 +189,36 @@ def test_prefill_config_full_size(gpu, name):
         for r in picks:
             if r0 <= r < r1:
                 kept[r] = lg[r - r0].cpu().numpy()
+        worst_all = 0.0
+        for c0 in range(r0, r1, chunk):
+            c1 = min(r1, c0 + chunk)
+            ref, mag, dmag = _ref_logits_gpu(q8[c0:c1], w[c0:c1], k8, ks, lens[c0:c1])
+            worst_all = max(worst_all, _check_logits_gpu(lg[c0 - r0:c1 - r0], ref, mag, dmag,
+                                                         f"{name} rows {c0}..{c1 - 1}"))
+            for r in picks:  # the GPU restatement is the CPU oracle's closed form
+                if c0 <= r < c1:
+                    L = int(case.lens[r])
+                    kept_ref = (ref[r - c0, :L].cpu().numpy(), mag[r - c0, :L].cpu().numpy())
+                    kept[("ref", r)] = kept_ref
+            del ref, mag, dmag
         del lg, want
-        _log(f"{name}: slab {s} ({r1 - r0} rows) top-k rows exact")
+        _log(f"{name}: slab {s} ({r1 - r0} rows) top-k rows exact; every logit within tolerance "
+             f"(worst error / magnitude {worst_all:.2e})")
 
     idx = np.array(picks)
     rq8, rw = O.quant_q(q_bits(case.q[idx]), case.w[idx].numpy())
-    assert np.array_equal(q8[idx].view(torch.uint8).cpu().numpy(), rq8), "q8 differs from the oracle"
-    assert np.array_equal(w[idx].cpu().numpy().view(np.uint32), rw.view(np.uint32)), "folded weights differ"
-    codes, scale = O.kv_tokens(kv_np(case.kv), O.slots_of(case.block_table.numpy(), width))
     sel = out[idx].cpu().numpy()
     worst = 0.0
     for i, r in enumerate(picks):
         L = int(case.lens[r])
-        ref, mag = O.logits_row(rq8[i], rw[i], codes[:L], scale[:L])
-        wm, _ = check_logits(kept[r][:L], ref, mag, f"{name} row {r}")
+        ref, mag, dmag = O.logits_row(rq8[i], rw[i], codes[:L], scale[:L])
+        gref, gmag = kept[("ref", r)]
+        # the same fp64 sums in another order: within a few ulps of the magnitude (the logit itself
+        # may cancel)
+        d = float((np.abs(gref - ref) / np.maximum(mag, 1e-300)).max())
+        assert d <= 1e-12 and np.allclose(gmag, mag, rtol=1e-12, atol=1e-300), \
+            f"{name} row {r}: the GPU fp64 restatement differs from indexer.logits_row ({d:.2e} of the magnitude)"
+        wm, _ = check_logits(kept[r][:L], ref, mag, dmag, f"{name} row {r}")
         worst = max(worst, wm)
         want = topk_radix(kept[r][None, :], None, np.array([L], dtype=np.int32), pt.numpy()[None, :], width)
         assert np.array_equal(sel[i], want[0]), f"{name}: row {r} differs from the oracle"

@@ -27,13 +27,13 @@ def _run_decode(case, gpu, pctas=0, rpc=None, hist=False):
 
 def _check_decode(case, lg, mask):
     q8, w = oracle_q(case)
-    ref, mag, ref_mask = oracle_decode(case, q8, w)
+    ref, mag, dmag, ref_mask = oracle_decode(case, q8, w)
     got_mask = mask.cpu().numpy()
     assert np.array_equal(got_mask, ref_mask), "nonzero mask differs"
     got = lg.cpu().numpy()
     for r in range(case.rows):
         L = int(case.context_lens[r])
-        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"row {r}")
 
 
 @pytest.mark.parametrize("heads", [64, 32])
@@ -182,11 +182,11 @@ def test_prefill_logits(gpu, heads, n_q, prefix):
     bt = torch.cat([case.block_table, torch.zeros(1, dtype=torch.int32)])  # capacity for width
     lg = hcu_ops.mqa_logits_prefill(q8, w, case.kv.to(gpu), bt.to(gpu), case.lens.to(gpu), width)
     rq8, rw = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
-    ref, mag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), bt.numpy(), case.lens.numpy(), width)
+    ref, mag, dmag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), bt.numpy(), case.lens.numpy(), width)
     got = lg.cpu().numpy()
     for r in range(case.rows):
         L = int(case.lens[r])
-        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"row {r}")
 
 
 def test_prefill_writes_only_below_len(gpu):
@@ -256,11 +256,11 @@ def test_prefill_wide_block_nontemporal_stores(gpu):
            lens.data_ptr(), out.data_ptr(), out.stride(0), width, torch.cuda.current_stream().cuda_stream)
     assert st == 0, lib.dsa_last_error()
     rq8, rw = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
-    ref, mag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), bt.numpy(), case.lens.numpy(), case.n_keys)
+    ref, mag, dmag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), bt.numpy(), case.lens.numpy(), case.n_keys)
     got = out.cpu().numpy()
     for r in range(case.rows):
         L = int(case.lens[r])
-        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"row {r}")
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"row {r}")
         assert np.isnan(got[r, L:]).all(), f"row {r}: entries past len written"
 
 

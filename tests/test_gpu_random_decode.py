@@ -49,12 +49,12 @@ def test_random_decode_step(gpu, seed):
                                              torch.arange(case.rows + 1, dtype=torch.int32, device=gpu))
     rq8, rw = oracle_q(case)
     assert np.array_equal(q8.view(torch.uint8).cpu().numpy(), rq8), f"{what}: q8"
-    ref, mag, ref_mask = oracle_decode(case, rq8, rw)
+    ref, mag, dmag, ref_mask = oracle_decode(case, rq8, rw)
     got_mask = mask.cpu().numpy()
     assert np.array_equal(got_mask, ref_mask), f"{what}: mask"
     got = lg.cpu().numpy()
     for r in range(case.rows):
         L = int(case.context_lens[r])
-        check_logits(got[r, :L], ref[r, :L], mag[r, :L], f"{what} row {r}")
+        check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"{what} row {r}")
     want = topk_radix(got.astype(np.float32), got_mask, case.context_lens.numpy(), pt.numpy(), case.width)
     assert np.array_equal(out.cpu().numpy(), want), f"{what}: top-k rows"

@@ -51,10 +51,10 @@ def test_random_prefill_indexer(gpu, seed):
 
     rq8, rw = O.quant_q(q_bits(case.q), case.w.numpy())
     assert np.array_equal(q8.view(torch.uint8).cpu().numpy(), rq8), f"{what}: q8"
-    ref, mag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), case.block_table.numpy(), case.lens.numpy(), width)
+    ref, mag, dmag = O.mqa_logits_prefill(rq8, rw, kv_np(case.kv), case.block_table.numpy(), case.lens.numpy(), width)
     for r in range(rows):
         L = int(case.lens[r])
-        check_logits(lg[r, :L], ref[r, :L], mag[r, :L], f"{what} row {r}")
+        check_logits(lg[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"{what} row {r}")
     want = topk_radix(lg.astype(np.float32), None, case.lens.numpy(), pt.numpy()[None, :], width,
                       cu_seqlens_q=np.array([0, rows], dtype=np.int32))
     assert np.array_equal(out.cpu().numpy(), want), f"{what}: top-k rows"

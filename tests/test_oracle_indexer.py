@@ -146,7 +146,7 @@ def _torch_logits(case, r):
 def test_logits_oracle_matches_torch_fp32():
     case = wl.decode_case(21, [700, 1500], group=2, heads=64)
     q8, w = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
-    lg, mag, mask = O.mqa_logits_decode(q8, w, _kv_np(case), case.context_lens.numpy(), case.block_table.numpy(),
+    lg, mag, _, mask = O.mqa_logits_decode(q8, w, _kv_np(case), case.context_lens.numpy(), case.block_table.numpy(),
                                         case.group, case.width)
     for r in range(case.rows):
         L = int(case.context_lens[r])
@@ -167,7 +167,7 @@ def test_logits_oracle_pure_python_tiny():
     k8[(k8 & 0x7F) == 0x7F] = 0
     w = rng.standard_normal(H).astype(np.float32)
     s = rng.random(n).astype(np.float32)
-    lg, _ = O.logits_row(q8, w, k8, s)
+    lg, _, _ = O.logits_row(q8, w, k8, s)
     qv, kv = fp8_decode(q8).tolist(), fp8_decode(k8).tolist()
     for t in range(n):
         tot = 0.0
@@ -185,16 +185,16 @@ def test_logits_linear_in_weights_and_scale():
     k8 = rng.integers(0, 126, (40, 128)).astype(np.uint8) ^ (rng.integers(0, 2, (40, 128)) * 0x80).astype(np.uint8)
     w1, w2 = rng.standard_normal(8).astype(np.float32), rng.standard_normal(8).astype(np.float32)
     s = rng.random(40).astype(np.float32)
-    a, _ = O.logits_row(q8, w1, k8, s)
-    b, _ = O.logits_row(q8, w2, k8, s)
-    c, _ = O.logits_row(q8, (w1.astype(np.float64) + w2).astype(np.float32), k8, s)
+    a, _, _ = O.logits_row(q8, w1, k8, s)
+    b, _, _ = O.logits_row(q8, w2, k8, s)
+    c, _, _ = O.logits_row(q8, (w1.astype(np.float64) + w2).astype(np.float32), k8, s)
     assert np.allclose(a + b, c, rtol=1e-6, atol=1e-6)
-    d, _ = O.logits_row(q8, w1, k8, (2 * s).astype(np.float32))
+    d, _, _ = O.logits_row(q8, w1, k8, (2 * s).astype(np.float32))
     assert np.array_equal(d, 2 * a)
     # all dot products negative -> relu kills everything -> exact zeros (mask bit clear)
     neg = np.full((8, 128), 0x38, dtype=np.uint8)  # +1.0
     kneg = np.full((3, 128), 0xB8, dtype=np.uint8)  # -1.0
-    z, _ = O.logits_row(neg, w1, kneg, s[:3])
+    z, _, _ = O.logits_row(neg, w1, kneg, s[:3])
     assert np.all(z == 0.0)
 
 
@@ -325,7 +325,7 @@ def test_cpu_baseline_row_matches_oracle():
     case = wl.decode_case(31, [5000], group=1, heads=64)
     q8, w = O.quant_q(case.q.view(torch.int16).numpy().view(np.uint16), case.w.numpy())
     kv = _kv_np(case)
-    lg, _, mask = O.mqa_logits_decode(q8, w, kv, case.context_lens.numpy(), case.block_table.numpy(), 1, case.width)
+    lg, _, _, mask = O.mqa_logits_decode(q8, w, kv, case.context_lens.numpy(), case.block_table.numpy(), 1, case.width)
     pt = case.page_table_1().numpy()
     ref = O.topk_transform(lg.astype(np.float32), mask, case.context_lens.numpy(), pt, case.width)
     slots = O.slots_of(case.block_table.numpy()[0], 5000)
@@ -349,14 +349,35 @@ def test_prefill_oracle_equals_decode_oracle_with_one_group():
     lens = case.lens.numpy().copy()
     lens[2] = 0
     lens[5] = width + 50  # clamped to the width by both
-    pre, pre_mag = O.mqa_logits_prefill(q8, w, kv, bt, lens, width)
+    pre, pre_mag, pre_dmag = O.mqa_logits_prefill(q8, w, kv, bt, lens, width)
     bt2 = np.tile(bt, (case.rows, 1))
-    dec, dec_mag, _ = O.mqa_logits_decode(q8, w, kv, lens, bt2, case.rows, width)
+    dec, dec_mag, dec_dmag, _ = O.mqa_logits_decode(q8, w, kv, lens, bt2, case.rows, width)
     assert np.array_equal(np.isnan(pre), np.isnan(dec))
     assert np.array_equal(pre[~np.isnan(pre)], dec[~np.isnan(dec)]) and np.array_equal(pre_mag, dec_mag)
+    assert np.array_equal(pre_dmag, dec_dmag)
     # and a causal row sees exactly its prefix: row i's logits are row j's on their common keys
     L3, L4 = int(lens[3]), int(lens[4])
     assert L3 < L4 and np.isnan(pre[3, L3:]).all() and not np.isnan(pre[4, :L4]).any()
+
+
+def test_logits_row_dot_magnitude_brute_force():
+    """M_t = s_t sum_h |w_h| sum_d |q8_hd k8_td| by plain loops on a small case, and
+    |logit| <= A_t <= M_t."""
+    rng = np.random.default_rng(3)
+    q8 = rng.integers(0, 256, size=(3, 128)).astype(np.uint8)
+    q8[(q8 & 0x7F) == 0x7F] = 0x20  # no NaN codes
+    k8 = rng.integers(0, 256, size=(5, 128)).astype(np.uint8)
+    k8[(k8 & 0x7F) == 0x7F] = 0x31
+    w = rng.normal(size=3).astype(np.float32)
+    s = rng.uniform(0.1, 2.0, size=5).astype(np.float32)
+    lg, mag, dmag = O.logits_row(q8, w, k8, s)
+    qv, kv = fp8_decode(q8).astype(np.float64), fp8_decode(k8).astype(np.float64)
+    for t in range(5):
+        m = 0.0
+        for h in range(3):
+            m += abs(float(w[h])) * sum(abs(qv[h, d] * kv[t, d]) for d in range(128))
+        assert abs(dmag[t] - m * float(s[t])) <= 1e-12 * dmag[t]
+        assert abs(lg[t]) <= mag[t] * (1 + 1e-12) and mag[t] <= dmag[t] * (1 + 1e-12)
 
 
 def test_quant_fmax_ignores_nan():
