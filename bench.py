@@ -219,6 +219,28 @@ class PrefillStep:
                 self.h.mqa_logits_prefill(self._q8[r0:r1], self._w8[r0:r1], self.kv, self.bt, self.lens[r0:r1],
                                           self.width)
 
+    def topk_us(self, torch):
+        """Live duration of each slab's top-k launch (the step's: one CTA per row of the slab's
+        logits, the request's page-table row shared), in graphs of 5 launches on logits made once
+        beforehand; with the algorithmic bytes of each (scores read once, 2048 page-table entries
+        gathered and written per row)."""
+        if not hasattr(self, "_q8"):
+            self._q8, self._w8 = self.h.quant_q_fp8(self.q, self.w)
+        pt = self.pt.unsqueeze(0)
+        res = []
+        for r0, r1 in self.slabs():
+            lg = self.h.mqa_logits_prefill(self._q8[r0:r1], self._w8[r0:r1], self.kv, self.bt, self.lens[r0:r1],
+                                           self.width)
+            lens = self.lens[r0:r1]
+            cu = torch.tensor([0, r1 - r0], dtype=torch.int32, device=lg.device)
+            out = torch.empty(r1 - r0, 2048, dtype=torch.int32, device=lg.device)
+            ms = kernel_time_ms(lambda: self.h.topk_transform(lg, lens, pt, cu, out=out), torch, reps=5, rounds=3,
+                                settle_ms=20.0)
+            nbytes = int(self.case.lens[r0:r1].clamp(max=self.width).long().sum()) * 4 + (r1 - r0) * 2048 * 8
+            res.append((ms * 1e3, nbytes))
+            del lg, out
+        return res
+
     def tokens(self):
         return self.case.tokens_scored()
 
@@ -517,6 +539,14 @@ def run_indexer(name, args, torch, dev, steps=None):
         measured["logits_frac_of_mfma_only"] = round(achieved / measured["mfma_only"], 4)
         measured["logits_frac_of_mfma_with_epilogue_valu"] = round(achieved / measured["mfma_with_epilogue_valu"], 4)
         roofline["measured_ceiling"] = measured
+        tk = step.topk_us(torch)
+        tk_us = sum(u for u, _ in tk)
+        tk_b = sum(b for _, b in tk)
+        roofline["slab_topk"] = {"kernel": "topk_row_sampled_kernel", "us_per_slab": [round(u, 1) for u, _ in tk],
+                                 "achieved_gbs": round(tk_b / (tk_us / 1e6) / 1e9, 1),
+                                 "frac_of_hbm": round(tk_b / (tk_us / 1e6) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "algorithmic_bytes": tk_b}
+        log(f"{name}: slab top-k {[round(u, 1) for u, _ in tk]} us")
         log(f"{name}: measured fp8 MFMA ceiling {measured['mfma_only']} TFLOP/s alone, "
             f"{measured['mfma_with_epilogue_valu']} with the epilogue's VALU work")
         pf = step.path_flops()
