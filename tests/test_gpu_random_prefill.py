@@ -58,3 +58,24 @@ def test_random_prefill_indexer(gpu, seed):
     want = topk_radix(lg.astype(np.float32), None, case.lens.numpy(), pt.numpy()[None, :], width,
                       cu_seqlens_q=np.array([0, rows], dtype=np.int32))
     assert np.array_equal(out.cpu().numpy(), want), f"{what}: top-k rows"
+
+
+@pytest.mark.parametrize("rows,prefix,slab", [(600, 1500, 600), (700, 5000, 560), (1100, 20000, 1024)])
+def test_prefill_indexer_medium_slabs(gpu, rows, prefix, slab):
+    """Slabs of hundreds of rows (one top-k CTA a row) and a smaller tail slab through
+    prefill_indexer, the rows' keys on both sides of 2048 and 4096, against the oracle's selection
+    on the same logits."""
+    case = wl.prefill_case(7000 + rows, rows, prefix, heads=64)
+    width = case.n_keys
+    g = lambda t: t.to(gpu)
+    kv, bt, lens = g(case.kv), g(case.block_table), g(case.lens)
+    q8, w = hcu_ops.quant_q_fp8(g(case.q), g(case.w))
+    pt = case.slots()
+    out = hcu_ops.prefill_indexer(q8, w, kv, bt, lens, width, g(pt), memory_budget_bytes=slab * width * 4,
+                                  max_slab_rows=slab)
+    lg = hcu_ops.mqa_logits_prefill(q8, w, kv, bt, lens, width).cpu().numpy()
+    want = topk_radix(lg.astype(np.float32), None, case.lens.numpy(), pt.numpy()[None, :], width,
+                      cu_seqlens_q=np.array([0, rows], dtype=np.int32))
+    got = out.cpu().numpy()
+    bad = [r for r in range(rows) if not np.array_equal(got[r], want[r])]
+    assert not bad, f"rows {bad[:8]} of {rows} (prefix {prefix}, slab {slab}) differ from the oracle"
