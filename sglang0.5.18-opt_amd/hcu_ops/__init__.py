@@ -33,13 +33,17 @@ _TOPK_SPLITS = int(os.environ.get("HCU_TOPK_SPLITS", "8"))
 #   HCU_MQA_PAIR_MAX_ROWS (this build's addition) otherwise, up to this many rows, the logits kernel
 #                        only zeroes the paired split top-k's per-row counters on its way, which saves
 #                        the top-k its zeroing launch; the top-k then selects against its sampled
-#                        threshold.  Measured on gfx950 for the 64-request MTP decode (G = 2): the
-#                        fused histogram's 8 KB of LDS counters per row cost the logits kernel more
-#                        occupancy than the histogram saves the top-k, hence 0 for grouped rows.
+#                        threshold.  Measured on gfx950, the fused histogram loses everywhere, hence
+#                        0 for both (the reference fuses up to 8 single rows): its 8 KB of LDS
+#                        counters per row cost the logits kernel occupancy, and the exact-bin top-k
+#                        after it is slower than the sampled one.  Decode steps (logits + top-k) of
+#                        1 / 8 single rows of 65,536 tokens, H = 64: 86.7 / 116.3 us fused,
+#                        24.7 / 34.2 us with the counters only; the 64-request MTP decode (G = 2):
+#                        logits 54.8 -> 58.7 us fused.
 _MQA_PCTAS = int(os.environ.get("HCU_MQA_PCTAS", "0"))
 _MQA_PCTAS_G1 = int(os.environ.get("HCU_MQA_PCTAS_G1", str(_MQA_PCTAS)))
 _MQA_RPC = int(os.environ.get("HCU_MQA_RPC", "2"))
-_MQA_HIST_MAX_ROWS = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS", "8"))
+_MQA_HIST_MAX_ROWS = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS", "0"))
 _MQA_HIST_MAX_ROWS_G6 = int(os.environ.get("HCU_MQA_HIST_MAX_ROWS_G6", "0"))
 _MQA_PAIR_MAX_ROWS = int(os.environ.get("HCU_MQA_PAIR_MAX_ROWS", "256"))
 _MQA_HIST = None  # (logits, hist_lens, zws, pass1_done) of the last mqa_logits with hist_lens
