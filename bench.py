@@ -58,6 +58,8 @@ WORKLOADS = {
     "dequant_mla_393k": "MLA K-cache dequant, 392832 tokens gathered at random from 2^19 656-B slots -> bf16 [n, 576]",
     "dequant_mla_131k": "MLA K-cache dequant, 131072 tokens gathered at random from 2^19 656-B slots -> bf16 [n, 576]",
     "dequant_k_74k": "indexer K dequant, the 73728 keys of prefill_8k_64k from the 132-B paged cache -> bf16 [n, 128]",
+    "reference_shapes": "per-call times at the shapes the reference publishes numbers for (BW1100, 32 heads): "
+                        "logits G=6 / G=1 at 16K-128K, split top-2048 of 6-192 relu_sum rows in a 1M-wide block",
 }
 DEQUANT_METRIC = "paged K-cache dequant, algorithmic GB/s (slot index + slot bytes read, bf16 written)"
 
@@ -585,6 +587,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true",
                     help="the default decode_mtp64 line only (no objects for the other workloads)")
+    ap.add_argument("--no-reference-shapes", action="store_true",
+                    help="no reference_shapes object (the reference's published shapes) in the default line")
     ap.add_argument("--no-dequant", action="store_true", help="no dequant objects (dequant_k_74k, dequant_mla_393k) in the default line")
     ap.add_argument("--steps-per-graph", type=int, default=10, help="steps captured in one hipGraph")
     ap.add_argument("--replays", type=int, default=20,
@@ -611,6 +615,11 @@ def main(argv=None):
         torch.cuda.synchronize()
         log(f"copy calibration: 3 copies of {args.copy_calibration_mib} MiB")
         del src, dst
+    if args.workload == "reference_shapes":
+        print(json.dumps({"metric": "per-call time at the reference's published shapes", "unit": "us",
+                          "higher_is_better": False, "n_gpus": 1, "data": "synthetic (seeded)",
+                          **run_reference_shapes(torch, dev)}), flush=True)
+        return 0
     if args.workload.startswith("dequant"):
         d = run_dequant(args.workload, args, torch, dev)
         line = {"metric": DEQUANT_METRIC, "value": d["value"], "unit": "GB/s", "n_gpus": 1, "steps": d["steps"],
@@ -640,8 +649,74 @@ def main(argv=None):
         if not args.no_dequant:
             for name in ("dequant_k_74k", "dequant_mla_393k"):
                 line[name] = {"metric": DEQUANT_METRIC, "unit": "GB/s", **run_dequant(name, args, torch, dev)}
+        if not args.no_reference_shapes:
+            line["reference_shapes"] = run_reference_shapes(torch, dev)
     print(json.dumps(line), flush=True)
     return 0
+
+
+# The reference's published per-call times (Hygon BW1100, 32 indexer heads, graph replays):
+# docs/GLM5.3_DCU_优化报告_20261023.md:395-403 (logits), docs/GLM5.3_opt2_README_20261023.md:158-162 (top-k).
+REF_LOGITS = [  # (group, requests, context, BW1100 us)
+    (6, 1, 16384, 21.6), (6, 4, 16384, 46.0), (6, 8, 16384, 73.8), (6, 1, 65536, 43.3), (6, 2, 65536, 71.5), (6, 4, 65536, 121.1), (6, 8, 65536, 210.9),
+    (6, 1, 131072, 72.5), (6, 2, 131072, 121.0),
+    (1, 1, 65536, 20.3), (1, 2, 65536, 21.8), (1, 4, 65536, 39.0), (1, 8, 65536, 73.0),
+]
+REF_TOPK = [  # (rows, context, BW1100 us), relu_sum rows in a 2^20-wide block
+    (6, 16384, 48.0), (6, 65536, 49.0), (6, 131072, 61.0), (12, 65536, 61.0), (24, 65536, 88.0),
+    (48, 65536, 116.0), (48, 131072, 211.0), (192, 16384, 127.0), (192, 65536, 341.0), (192, 131072, 626.0),
+]
+
+
+def run_reference_shapes(torch, dev):
+    """MI355X per-call times at the reference's published shapes, beside its BW1100 numbers:
+    the decode logits launch (32 heads, MTP groups of 6 rows with context L + j for row j, or single
+    rows; paired with the top-k's workspace as in a step) and the split top-2048 + page-table
+    transform of relu_sum rows (8 ReLU'd normals with one weight vector, the reference's test
+    distribution) of ragged lengths L - 37 i - 3 in a 2^20-wide block.  Context only: the
+    reference's hardware and head count differ."""
+    import hcu_ops as h
+    import workloads as wl
+    logits = []
+    for group, n_req, L, ref_us in REF_LOGITS:
+        case = wl.decode_case(900 + group * 10 + n_req, [L] * n_req, group=group, heads=32)
+        g = lambda t: t.to(dev)
+        q8, w = h.quant_q_fp8(g(case.q), g(case.w))
+        kv, lens, bt = g(case.kv), g(case.context_lens), g(case.block_table)
+        ms = kernel_time_ms(lambda: h.mqa_logits(q8.unsqueeze(1), kv, w, lens, bt, case.width, group, hist_lens=lens),
+                            torch, reps=10, rounds=5, settle_ms=20.0)
+        logits.append({"group": group, "requests": n_req, "context": L, "mi355x_us": round(ms * 1e3, 1),
+                       "bw1100_us": ref_us})
+        del case, q8, w, kv, lens, bt
+    topk = []
+    W = 1 << 20
+    gen = torch.Generator(device=dev)
+    for rows, L, ref_us in REF_TOPK:
+        gen.manual_seed(rows * 7 + L)
+        c = torch.rand(8, generator=gen, device=dev) - 0.3
+        x = torch.full((rows, W), float("nan"), device=dev)
+        for r in range(rows):
+            x[r, :L] = (torch.relu(torch.randn(L, 8, generator=gen, device=dev)) * c).sum(-1)
+        nz = ~torch.isnan(x) & (x != 0)
+        x = torch.where(nz, x, torch.full_like(x, float("nan")))
+        w16 = (1 << torch.arange(16, device=dev, dtype=torch.int32))
+        bits = (nz.view(rows, -1, 16).to(torch.int32) * w16).sum(-1, dtype=torch.int32)
+        mask = torch.where(bits > 32767, bits - 65536, bits).to(torch.int16).contiguous()
+        del nz, bits
+        lengths = (L - torch.arange(rows, device=dev) * 37 - 3).clamp(min=1).to(torch.int32)
+        pt = (torch.arange(W, dtype=torch.int32, device=dev).unsqueeze(0) + 7
+              + 1000000 * torch.arange(rows, dtype=torch.int32, device=dev).unsqueeze(1)).contiguous()
+        cu = torch.arange(rows + 1, dtype=torch.int32, device=dev)
+        ms = kernel_time_ms(lambda: h.sparse_mask_topk_transform(x, mask, lengths, pt, cu), torch, reps=10, rounds=5,
+                            settle_ms=20.0)
+        topk.append({"rows": rows, "context": L, "width": W, "mi355x_us": round(ms * 1e3, 1), "bw1100_us": ref_us})
+        del x, mask, pt
+        torch.cuda.empty_cache()
+    log(f"reference shapes: logits {[(d['group'], d['requests'], d['context'], d['mi355x_us']) for d in logits]}")
+    log(f"reference shapes: top-k {[(d['rows'], d['context'], d['mi355x_us']) for d in topk]}")
+    return {"logits_32_heads": logits, "topk_2048_relu_sum_1m_wide": topk,
+            "note": "per call, graphs of 10 launches, median of 5; MI355X with this build beside the reference's "
+                    "published BW1100 (gfx938, 64 CUs) numbers for its hcu kernels; context, not a target"}
 
 
 def run_dequant(name, args, torch, dev):
