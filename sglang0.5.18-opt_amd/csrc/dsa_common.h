@@ -81,8 +81,12 @@ __device__ __forceinline__ float quant_vec16(const uint16_t* src, int sub, uint3
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  // max over the 16 lanes (one DPP row) without LDS: lane ^ 1, lane ^ 2 (quad_perm), then the
+  // row's half mirror (lane i <-> 7 - i within 8) and mirror (i <-> 15 - i)
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x141, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x140, 0xF, 0xF, false)));
   float inv;
   quant_factors(amax, inv, scale);
   uint32_t c[8];

@@ -27,11 +27,13 @@ __global__ __launch_bounds__(kQThreads) void quant_q_kernel(const uint16_t* __re
   const int64_t v = static_cast<int64_t>(blockIdx.x) * kVecPerCta + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   if (v >= n_vec) return;  // whole 16-lane groups drop out together
+  // the weight's load goes out beside q's (used only by lane 0 it was issued after q's round trip)
+  const float wv = w[v];
   u32x2 packed;
   float scale;
   quant_vec(q + v * kHeadDim, sub, packed, scale);
   *reinterpret_cast<u32x2*>(q8 + v * kHeadDim + sub * 8) = packed;
-  if (sub == 0) w_eff[v] = w[v] * scale;
+  w_eff[v] = wv * scale;  // the 16 lanes store one value to one address
 }
 
 __global__ __launch_bounds__(kQThreads) void store_k_kernel(const uint16_t* __restrict__ k, int64_t n,
