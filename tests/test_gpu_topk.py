@@ -75,6 +75,38 @@ def test_topk_production_width(gpu, dist):
         del xg, mg, pg
 
 
+def _sample_chunks(L):
+    """First tokens of the 256 sampled 16-token chunks of a row longer than 4096 tokens (the
+    kernel's fixed sample: chunk c starts at ((2c + 1) L / 512) rounded down to 16)."""
+    c = np.arange(256)
+    return np.minimum((((2 * c + 1) * L) // 512) & ~15, (L - 16) & ~15)
+
+
+@pytest.mark.parametrize("target", [4600, 7000])
+def test_topk_wide_rows_sample_misses(gpu, target):
+    """Rows of 131,072 tokens (scores wider than 80K: the one-CTA-per-row kernel with its larger
+    candidate list) whose sample sits in a narrow band low in the row's distribution, so that the
+    sample's threshold collects about `target` keys: 4600 lies past 4096 but within the wide
+    list, 7000 past it (the exact path).  The set and order must equal the oracle's either way
+    (U(0, 1) scores, the sample's tokens in [t, t + 1e-3] with t leaving ~target keys above)."""
+    L, B = 131072, 4
+    g = torch.Generator().manual_seed(target)
+    x = torch.rand(B, L, generator=g) * 0.999 + 0.001
+    t = 1.0 - target / L
+    idx = torch.from_numpy((_sample_chunks(L)[:, None] + np.arange(16)[None, :]).reshape(-1))
+    for r in range(B):
+        x[r, idx] = t + torch.rand(idx.numel(), generator=g) * 1e-3
+    w16 = torch.tensor([1 << i for i in range(16)], dtype=torch.int32)
+    bits = (torch.ones(B, L // 16, 16, dtype=torch.int32) * w16).sum(-1, dtype=torch.int32)
+    mask = torch.where(bits > 32767, bits - 65536, bits).to(torch.int16).contiguous()
+    lengths = torch.tensor([L, L - 5, L - 4096, L - 77], dtype=torch.int32)
+    pt = (torch.arange(L, dtype=torch.int32)[None, :] + 11 + 1000000 * torch.arange(B, dtype=torch.int32)[:, None])
+    ref = np.asarray(_oracle(x, mask, lengths, pt, L))
+    cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
+    got = IMPLS["single"](x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu), cu)
+    assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"target {target}"
+
+
 def test_topk_many_rows_and_empty(gpu):
     x, mask, lengths, pt = wl.topk_scores(600, 5000, "relu_sum", W=5056, ragged=True, seed=1)
     ref = np.asarray(_oracle(x, mask, lengths, pt, 5056))
