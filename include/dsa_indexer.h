@@ -196,6 +196,21 @@ int dsa_topk_transform_pre(const float* score, int64_t score_stride, int64_t wid
                            int32_t* hist_ws, int pass1_done, void* workspace, size_t workspace_bytes,
                            int32_t* out, hipStream_t stream);
 
+/* dsa_topk_transform / dsa_topk_transform_pre (hist_ws nullable) with the page table given as
+ * the block table it expands (an optional form with no counterpart in the reference, whose
+ * sparse_mask_topk.cu:348,751,804-807 gather page_table_size_1[row][t]): token t of a row maps
+ * to block_table[row][t / 64] * 64 + t % 64, the entry page_table_size_1 holds when it is the
+ * expansion of the 64-token-page block table, and tokens t >= bt_pages * 64 map to -1.
+ * block_table [rows or n_req, bt_pages] i32 with row stride bt_stride (0: one row for all).
+ * For callers that hold the block table: the transform reads 4 B per 64 tokens instead of 4 B
+ * per token.  Same results as dsa_topk_transform on the expanded table. */
+int dsa_topk_transform_blocks(const float* score, int64_t score_stride, int64_t width,
+                              const int16_t* mask, int64_t mask_stride, const int32_t* lengths,
+                              int64_t rows, const int32_t* block_table, int64_t bt_stride, int64_t bt_pages,
+                              const int32_t* cu_seqlens_q, int64_t n_req, int max_splits, int n_cu,
+                              int32_t* hist_ws, int pass1_done, void* workspace, size_t workspace_bytes,
+                              int32_t* out, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Prefill indexer of one request (the role of sglang's prefill indexer under
  * SGLANG_NSA_MQA_LOGITS_MEMORY_BUDGET_GB, prefill/p_opt.sh:58, at the cached-prefix call site

@@ -239,18 +239,26 @@ def topk_tokens(keys, k=TOPK):
 def topk_transform(score, mask, lengths, page_table, width, cu_seqlens_q=None):
     """Oracle of dsa_topk_transform: int32 [rows, 2048]; selected rows are returned as the
     page-table entries of the selected tokens in ascending token order (the contract is the
-    set), short rows as page_table[:len] then -1."""
+    set), short rows as page_table[:len] then -1.  Tokens past a page-table row's columns map
+    to -1 (the reference requires >= len columns; this build defines the rest)."""
     rows = score.shape[0]
     out = np.full((rows, TOPK), -1, dtype=np.int32)
+
+    def entries(pt, toks):
+        v = np.full(len(toks), -1, dtype=np.int32)
+        inside = toks < pt.shape[0]
+        v[inside] = pt[toks[inside]]
+        return v
+
     for r in range(rows):
         pr = r if cu_seqlens_q is None else int(np.searchsorted(cu_seqlens_q, r, side="right") - 1)
         L = int(np.clip(lengths[r], 0, width))
         pt = page_table[pr]
         if L <= TOPK:
-            out[r, :L] = pt[:L]
+            out[r, :L] = entries(pt, np.arange(L))
             continue
         keys = row_keys(score[r], None if mask is None else mask[r], L)
-        out[r] = pt[topk_tokens(keys)]
+        out[r] = entries(pt, topk_tokens(keys))
     return out
 
 

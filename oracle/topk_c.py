@@ -24,7 +24,7 @@ def _load():
         lib = ctypes.CDLL(LIB)
         P = ctypes.c_void_p
         lib.topk_radix.argtypes = [P, ctypes.c_int64, ctypes.c_int, P, ctypes.c_int64, P, ctypes.c_int, P,
-                                   ctypes.c_int64, P, ctypes.c_int, P]
+                                   ctypes.c_int64, ctypes.c_int, P, ctypes.c_int, P]
         lib.topk_radix.restype = None
         _lib = lib
     return _lib
@@ -41,5 +41,5 @@ def topk_radix(score, mask, lengths, page_table, width, cu_seqlens_q=None):
     cu = None if cu_seqlens_q is None else np.ascontiguousarray(cu_seqlens_q, dtype=np.int32)
     ptr = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)
     _load().topk_radix(ptr(score), score.shape[1], int(width), ptr(m), 0 if m is None else m.shape[1], ptr(lengths),
-                       rows, ptr(pt), pt.shape[1], ptr(cu), 0 if cu is None else cu.shape[0] - 1, ptr(out))
+                       rows, ptr(pt), pt.shape[1], pt.shape[1], ptr(cu), 0 if cu is None else cu.shape[0] - 1, ptr(out))
     return out

@@ -46,10 +46,14 @@ static int find_threshold(const int* hist, int nb, int need, int* above) {
   return 0; /* unreachable when sum(hist) >= need */
 }
 
-void topk_radix_row(const float* score, const int16_t* mask, int len, const int32_t* pt, int32_t* dst) {
+/* Page-table entry of token t: -1 past the row's pt_cols entries (a table narrower than the
+ * row; the reference requires >= len entries, this build maps the rest to -1). */
+static int32_t pt_at(const int32_t* pt, int pt_cols, int t) { return t < pt_cols ? pt[t] : -1; }
+
+void topk_radix_row(const float* score, const int16_t* mask, int len, const int32_t* pt, int pt_cols, int32_t* dst) {
   static int hist[4096];
   if (len <= TOPK) {
-    for (int i = 0; i < TOPK; ++i) dst[i] = i < len ? pt[i] : -1;
+    for (int i = 0; i < TOPK; ++i) dst[i] = i < len ? pt_at(pt, pt_cols, i) : -1;
     return;
   }
   memset(hist, 0, sizeof(hist));
@@ -96,16 +100,17 @@ void topk_radix_row(const float* score, const int16_t* mask, int len, const int3
   int a = 0, ties = 0;
   for (int t = 0; t < len; ++t) {
     const uint32_t key = token_key(score, mask, t);
-    if (key > thr) dst[a++] = pt[t];
-    else if (key == thr && ties < remaining) dst[tie_base + ties++] = pt[t];
+    if (key > thr) dst[a++] = pt_at(pt, pt_cols, t);
+    else if (key == thr && ties < remaining) dst[tie_base + ties++] = pt_at(pt, pt_cols, t);
   }
 }
 
 /* Batched entry: rows of score [rows, score_stride], mask [rows, mask_stride] (nullable),
- * page-table row pr = r (cu == NULL) or the request b with cu[b] <= r < cu[b + 1]. */
+ * page-table row pr = r (cu == NULL) or the request b with cu[b] <= r < cu[b + 1], pt_cols
+ * entries per page-table row. */
 void topk_radix(const float* score, int64_t score_stride, int width, const int16_t* mask, int64_t mask_stride,
-                const int32_t* lengths, int rows, const int32_t* pt, int64_t pt_stride, const int32_t* cu, int n_req,
-                int32_t* out) {
+                const int32_t* lengths, int rows, const int32_t* pt, int64_t pt_stride, int pt_cols, const int32_t* cu,
+                int n_req, int32_t* out) {
   for (int r = 0; r < rows; ++r) {
     int pr = r;
     if (cu != NULL) {
@@ -115,6 +120,6 @@ void topk_radix(const float* score, int64_t score_stride, int width, const int16
     int len = lengths[r];
     len = len < 0 ? 0 : (len < width ? len : width);
     topk_radix_row(score + (int64_t)r * score_stride, mask ? mask + (int64_t)r * mask_stride : NULL, len,
-                   pt + (int64_t)pr * pt_stride, out + (int64_t)r * TOPK);
+                   pt + (int64_t)pr * pt_stride, pt_cols, out + (int64_t)r * TOPK);
   }
 }

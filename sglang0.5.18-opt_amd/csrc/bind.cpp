@@ -124,7 +124,8 @@ void check_topk(const torch::Tensor& score, const c10::optional<torch::Tensor>& 
 torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::Tensor>& nonzero_mask,
                         const torch::Tensor& lengths, const torch::Tensor& page_table_size_1,
                         const torch::Tensor& cu_seqlens_q, int64_t topk, int64_t max_splits,
-                        const torch::Tensor* zws, bool pass1_done, const torch::Tensor* out = nullptr) {
+                        const torch::Tensor* zws, bool pass1_done, const torch::Tensor* out = nullptr,
+                        bool blocks = false) {
   check_topk(score, nonzero_mask, lengths, page_table_size_1, topk);
   const int64_t rows = score.size(0);
   const int64_t width = score.size(1);
@@ -159,6 +160,14 @@ torch::Tensor topk_impl(const torch::Tensor& score, const c10::optional<torch::T
   if (zws != nullptr) {
     TORCH_CHECK(zws->scalar_type() == at::kInt && zws->is_contiguous() && zws->numel() == rows * (2 * kBins + 2),
                 "zws must be the int32 [rows * (2 * 4096 + 2)] pass-1 workspace");
+  }
+  if (blocks) {
+    st = dsa_topk_transform_blocks(score.data_ptr<float>(), score.stride(0), width, mp, ms, lengths.data_ptr<int>(),
+                                   rows, page_table_size_1.data_ptr<int>(), page_table_size_1.stride(0),
+                                   page_table_size_1.size(1), cu, n_req, splits, cus,
+                                   zws != nullptr ? zws->data_ptr<int>() : nullptr, pass1_done ? 1 : 0,
+                                   ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, dst.data_ptr<int>(), cur_stream());
+  } else if (zws != nullptr) {
     st = dsa_topk_transform_pre(score.data_ptr<float>(), score.stride(0), width, mp, ms, lengths.data_ptr<int>(),
                                 rows, page_table_size_1.data_ptr<int>(), page_table_size_1.stride(0),
                                 page_table_size_1.size(1), cu, n_req,
@@ -195,6 +204,18 @@ torch::Tensor sparse_mask_topk_transform_split_pre(const torch::Tensor& score, c
                                                    bool pass1_done) {
   return topk_impl(score, nonzero_mask, lengths, page_table_size_1, cu_seqlens_q, topk, max_splits, &zws,
                    pass1_done);
+}
+
+// The same with the block table that page_table_size_1 expands (4 B per 64-token page): token t
+// maps to block_table[row][t / 64] * 64 + t % 64.  nonzero_mask None: dense scores.  zws:
+// optional pass-1 workspace of a paired logits call, as in sparse_mask_topk_transform_split_pre.
+torch::Tensor sparse_mask_topk_transform_blocks(const torch::Tensor& score,
+                                                const c10::optional<torch::Tensor>& nonzero_mask,
+                                                const torch::Tensor& lengths, const torch::Tensor& block_table,
+                                                const torch::Tensor& cu_seqlens_q, int64_t topk, int64_t max_splits,
+                                                const c10::optional<torch::Tensor>& zws, bool pass1_done) {
+  return topk_impl(score, nonzero_mask, lengths, block_table, cu_seqlens_q, topk, max_splits,
+                   zws.has_value() ? &*zws : nullptr, pass1_done, nullptr, true);
 }
 
 // Dense-score top-k (no sparse mask: every score below the row length is valid), e.g. prefill.
@@ -397,6 +418,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("score"), py::arg("nonzero_mask"), py::arg("lengths"), py::arg("page_table_size_1"),
         py::arg("cu_seqlens_q"), py::arg("topk"), py::arg("max_splits"), py::arg("zws"),
         py::arg("pass1_done") = true);
+  m.def("sparse_mask_topk_transform_blocks", &sparse_mask_topk_transform_blocks,
+        "sparse_mask_topk_transform_split[_pre] with the 64-token-page block table instead of page_table_size_1",
+        py::arg("score"), py::arg("nonzero_mask"), py::arg("lengths"), py::arg("block_table"),
+        py::arg("cu_seqlens_q"), py::arg("topk"), py::arg("max_splits"), py::arg("zws") = py::none(),
+        py::arg("pass1_done") = false);
   m.def("topk_transform", &topk_transform, "Exact top-2048 + page-table transform over dense scores (into out if given)",
         py::arg("score"), py::arg("lengths"), py::arg("page_table_size_1"), py::arg("cu_seqlens_q"), py::arg("topk"),
         py::arg("max_splits"), py::arg("out") = py::none());

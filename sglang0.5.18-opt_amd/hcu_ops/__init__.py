@@ -73,6 +73,24 @@ def sparse_mask_topk_transform(score, nonzero_mask, lengths, page_table_size_1, 
                                                _TOPK_SPLITS)
 
 
+def sparse_mask_topk_transform_blocks(score, nonzero_mask, lengths, block_table, cu_seqlens_q, topk=2048):
+    """sparse_mask_topk_transform with the 64-token-page block table that page_table_size_1 expands
+    (this build's addition; the reference gathers page_table_size_1[row][t]): token t maps to
+    block_table[row][t // 64] * 64 + t % 64, so the transform reads 4 B per 64 tokens instead of
+    4 B per token.  Pairs with a preceding mqa_logits(..., hist_lens=lengths) like the reference
+    form."""
+    global _MQA_HIST
+    st = _MQA_HIST
+    zws, done = None, False
+    if st is not None:
+        _MQA_HIST = None
+        if st[0] is score and st[1].data_ptr() == lengths.data_ptr() and st[1].shape == lengths.shape:
+            zws, done = st[2], st[3]
+    splits = 1 if _TOPK_IMPL == "single" and zws is None else _TOPK_SPLITS
+    return _C.sparse_mask_topk_transform_blocks(score, nonzero_mask, lengths, block_table, cu_seqlens_q, topk, splits,
+                                                zws, done)
+
+
 def mqa_logits_supported(q, kv_cache, weights, group_size, context_lens=None, block_table=None,
                          max_context_len=None):
     """Whether mqa_logits takes these operands (else the caller keeps its fallback)."""

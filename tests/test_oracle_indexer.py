@@ -296,6 +296,24 @@ def test_topk_varlen_layout():
     assert np.all(brute[3:6] >= 200000) and np.all(brute[0:2] < 100000)
 
 
+def test_topk_narrow_page_table():
+    """A page-table row narrower than the row: tokens past its columns map to -1 in both oracles
+    (brute force and the C radix), short rows included; the other entries are the table's."""
+    x, mask, lengths, _ = wl.topk_scores(4, 6000, "mixed", seed=4)
+    lengths = torch.tensor([6000, 5000, 1900, 4100], dtype=torch.int32)
+    x[0, 4000:6000] = torch.nan_to_num(x[0, 4000:6000]).abs() + 1000.0  # row 0 selects past the table
+    pt = (np.arange(4500)[None, :] * 3 + 7 + 100000 * np.arange(4)[:, None]).astype(np.int32)[:, :1800]
+    brute = O.topk_transform(x.numpy(), mask.numpy(), lengths.numpy(), pt, 6000)
+    rad = topk_radix(x.numpy(), mask.numpy(), lengths.numpy(), pt, 6000)
+    assert np.array_equal(np.sort(brute, 1), np.sort(rad, 1))
+    wide = (np.arange(6000)[None, :] * 3 + 7 + 100000 * np.arange(4)[:, None]).astype(np.int32)
+    full = O.topk_transform(x.numpy(), mask.numpy(), lengths.numpy(), wide, 6000)
+    expect = np.where((full - 7 - 100000 * np.arange(4)[:, None]) // 3 < 1800, full, -1)
+    expect[full == -1] = -1
+    assert np.array_equal(brute, expect)
+    assert (brute[0] == -1).sum() > 0 and (brute[2, 1800:1900] == -1).all()
+
+
 def test_pass1_hist_closed_form():
     """Histogram restated with torch ops exactly as hcu_ops/tests/test_mqa_hist.py:109-124."""
     x, mask, lengths, _ = wl.topk_scores(5, 6000, "relu_sum", W=8000, ragged=True, seed=2)
