@@ -96,11 +96,14 @@ def cpu_model():
 # Decode
 
 class DecodeStep:
-    def __init__(self, case, dev):
+    def __init__(self, case, dev, blocks=False):
+        """blocks: the top-k transform reads the block table (sparse_mask_topk_transform_blocks)
+        instead of its page_table_size_1 expansion (the reference's caller form, the default)."""
         import torch
         import hcu_ops
         self.h = hcu_ops
         self.case = case
+        self.blocks = blocks
         g = lambda t: t.to(dev)
         self.q, self.w, self.kv = g(case.q), g(case.w), g(case.kv)
         self.lens, self.bt = g(case.context_lens), g(case.block_table)
@@ -113,7 +116,10 @@ class DecodeStep:
         q8, w = h.quant_q_fp8(self.q, self.w)
         logits, mask = h.mqa_logits(q8.unsqueeze(1), self.kv, w, self.lens, self.bt, c.width, c.group,
                                     hist_lens=self.lens)
-        self.out = h.sparse_mask_topk_transform(logits, mask, self.lens, self.pt, self.cu)
+        if self.blocks:
+            self.out = h.sparse_mask_topk_transform_blocks(logits, mask, self.lens, self.bt, self.cu)
+        else:
+            self.out = h.sparse_mask_topk_transform(logits, mask, self.lens, self.pt, self.cu)
         return self.out
 
     def logits_only(self, hist=False):
@@ -571,8 +577,22 @@ def run_indexer(name, args, torch, dev, steps=None):
         config["dequant"] = ("none in the step: the logits kernel reads the paged fp8 K directly, so the bf16 "
                              "copy of K that the configuration names is never made (dequant_k_74k times that "
                              "dequant on its own)")
-    return {"value": round(value, 1), "ms_per_step": round(ms, 5), "steps": args.steps, "warmup": args.warmup,
-            "replays": stats, "config": config, "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu}
+    res = {"value": round(value, 1), "ms_per_step": round(ms, 5), "steps": args.steps, "warmup": args.warmup,
+           "replays": stats, "config": config, "roofline": roofline, "path_roofline": path, "cpu_baseline": cpu}
+    if decode:
+        # the same step with the top-k's page-table transform reading the block table the logits already
+        # use (dsa_topk_transform_blocks) instead of its page_table_size_1 expansion: same output
+        del step
+        bstep = DecodeStep(case, dev, blocks=True)
+        b_ms, _, b_stats = timed_steps(bstep, args, torch)
+        res["block_table_topk"] = {
+            "value": round(tokens / 1e3 / (b_ms / 1e3), 1), "unit": "K-tokens/s", "ms_per_step": round(b_ms, 5),
+            "replays": b_stats, "path_roofline_frac": round(bstep.path_bytes() / (b_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "the step with hcu_ops.sparse_mask_topk_transform_blocks (the top-k reads the block table, 4 B "
+                    "per 64 tokens, instead of page_table_size_1, 4 B per token); same output; value and "
+                    "ms_per_step above use the reference's page_table_size_1 form"}
+        log(f"{name}: with the block-table top-k {b_ms * 1e3:.1f} us/step")
+    return res
 
 
 def main(argv=None):
@@ -637,6 +657,8 @@ def main(argv=None):
             "data": "synthetic (seeded, see tests/workloads.py)", "config": head["config"],
             "replays": head["replays"], "roofline": head["roofline"], "path_roofline": head["path_roofline"],
             "cpu_baseline": head["cpu_baseline"]}
+    if "block_table_topk" in head:
+        line["block_table_topk"] = head["block_table_topk"]
     if args.workload == "decode_mtp64" and not args.no_prefill:
         # the second headline workload (the 64K-prefix chunked prefill) and the other configurations
         # in the same line, each with its own roofline and CPU baseline; prefill step counts sized
