@@ -154,7 +154,9 @@ int dsa_mqa_logits_prefill(const uint8_t* q8, const float* w, int heads, int64_t
  * mask_stride; lengths i32 [rows]; page_table i32 with pt_cols entries per row (tokens at or past
  * pt_cols map to -1) and row stride pt_stride (0: every row reads the same page-table row, e.g.
  * the query rows of one prefill request); out i32 [rows, 2048].
- * max_splits: CTAs a row may be split over (1 = one CTA per row).
+ * max_splits: CTAs a row may be split over (1 = one CTA per row).  Workspace: split rows need a
+ * candidate list of 4096 entries each, 5120 for scores wider than 81,920 tokens (0 bytes when no
+ * row is split).
  */
 size_t dsa_topk_workspace_bytes(int64_t rows, int64_t width, int max_splits, int n_cu);
 /* CTAs per row the top-k splits [rows, width] scores over (1: one CTA per row); the role of the
@@ -169,7 +171,8 @@ int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
 /* dsa_topk_transform without the workspace argument, for callers that cannot allocate device
  * memory (code under hipGraph capture with no allocator at hand, tight serving loops, harnesses
  * that forbid allocation).  No counterpart in the reference.  The split path's workspace is a
- * built-in device array of dsa_topk_noalloc_max_bytes() (8.0 MiB: up to 256 rows split) per device,
+ * built-in device array of dsa_topk_noalloc_max_bytes() (8.0 MiB: up to 256 rows split, 204 rows
+ * of scores wider than 81,920 tokens) per device,
  * held until the process ends; its address is looked up on the first call on each device.
  * Inputs needing a larger workspace (dsa_topk_workspace_bytes) are rejected with
  * DSA_ERR_WORKSPACE.  Every call on one device shares that device's array: calls that overlap on

@@ -161,6 +161,9 @@ def test_noalloc_topk_rejects_oversize_on_the_host(lib):
     assert cap == 4096 + 2 * 256 * 4096 * 4
     assert lib.dsa_topk_workspace_bytes(256, 65536, 8, 256) == cap
     assert lib.dsa_topk_workspace_bytes(300, 65536, 8, 256) > cap
+    # scores wider than 81,920 tokens: 5120-entry lists, so 204 split rows fit and 205 do not
+    assert lib.dsa_topk_workspace_bytes(204, 131072, 8, 256) <= cap < lib.dsa_topk_workspace_bytes(205, 131072, 8, 256)
+    assert lib.dsa_topk_workspace_bytes(204, 131072, 8, 256) > lib.dsa_topk_workspace_bytes(204, 81920, 8, 256)
     f = lib.dsa_topk_transform_noalloc
     f.argtypes = [P, I64, I64, P, I64, P, I64, P, I64, I64, P, I64, I, I, P, P]
     assert f(P(16), 65536, 65536, None, 0, P(16), 300, P(16), 65536, 65536, None, 300, 8, 256, P(16), None) == 2

@@ -84,8 +84,8 @@ def _sample_chunks(L):
 
 @pytest.mark.parametrize("target", [4600, 7000])
 def test_topk_wide_rows_sample_misses(gpu, target):
-    """Rows of 131,072 tokens (scores wider than 80K: the one-CTA-per-row kernel with its larger
-    candidate list) whose sample sits in a narrow band low in the row's distribution, so that the
+    """Rows of 131,072 tokens (scores wider than 80K: the one-CTA-per-row and split kernels with
+    their larger candidate list) whose sample sits in a narrow band low in the row's distribution, so that the
     sample's threshold collects about `target` keys: 4600 lies past 4096 but within the wide
     list, 7000 past it (the exact path).  The set and order must equal the oracle's either way
     (U(0, 1) scores, the sample's tokens in [t, t + 1e-3] with t leaving ~target keys above)."""
@@ -103,8 +103,9 @@ def test_topk_wide_rows_sample_misses(gpu, target):
     pt = (torch.arange(L, dtype=torch.int32)[None, :] + 11 + 1000000 * torch.arange(B, dtype=torch.int32)[:, None])
     ref = np.asarray(_oracle(x, mask, lengths, pt, L))
     cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
-    got = IMPLS["single"](x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu), cu)
-    assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"target {target}"
+    for name in ("single", "s2", "s8"):  # the row kernel and the split kernel, both with the wide list
+        got = IMPLS[name](x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu), cu)
+        assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"target {target} impl {name}"
 
 
 def test_topk_many_rows_and_empty(gpu):
