@@ -171,7 +171,7 @@ int dsa_topk_transform(const float* score, int64_t score_stride, int64_t width,
 /* dsa_topk_transform without the workspace argument, for callers that cannot allocate device
  * memory (code under hipGraph capture with no allocator at hand, tight serving loops, harnesses
  * that forbid allocation).  No counterpart in the reference.  The split path's workspace is a
- * built-in device array of dsa_topk_noalloc_max_bytes() (8.0 MiB: up to 256 rows split, 204 rows
+ * built-in device array of dsa_topk_noalloc_max_bytes() (12.0 MiB: up to 256 rows split, 204 rows
  * of scores wider than 81,920 tokens) per device,
  * held until the process ends; its address is looked up on the first call on each device.
  * Inputs needing a larger workspace (dsa_topk_workspace_bytes) are rejected with

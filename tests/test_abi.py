@@ -152,13 +152,13 @@ def test_reference_knob_gate(monkeypatch):
 
 def test_noalloc_topk_rejects_oversize_on_the_host(lib):
     """The allocation-free top-k refuses inputs whose split workspace exceeds its built-in array,
-    before touching a device: 300 rows of 64K split in two need ~9.8 MB."""
+    before touching a device: 300 rows of 64K split in two need ~14.7 MB."""
     P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     lib.dsa_topk_noalloc_max_bytes.restype = ctypes.c_size_t
     lib.dsa_topk_workspace_bytes.argtypes = [I64, I64, I, I]
     lib.dsa_topk_workspace_bytes.restype = ctypes.c_size_t
     cap = lib.dsa_topk_noalloc_max_bytes()
-    assert cap == 4096 + 2 * 256 * 4096 * 4
+    assert cap == 4096 + 3 * 256 * 4096 * 4  # counters, then keys, tokens and page-table entries of 256 rows
     assert lib.dsa_topk_workspace_bytes(256, 65536, 8, 256) == cap
     assert lib.dsa_topk_workspace_bytes(300, 65536, 8, 256) > cap
     # scores wider than 81,920 tokens: 5120-entry lists, so 204 split rows fit and 205 do not
