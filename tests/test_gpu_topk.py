@@ -87,8 +87,9 @@ def test_topk_wide_rows_sample_misses(gpu, target):
     """Rows of 131,072 tokens (scores wider than 80K: the one-CTA-per-row and split kernels with
     their larger candidate list) whose sample sits in a narrow band low in the row's distribution, so that the
     sample's threshold collects about `target` keys: 4600 lies past 4096 but within the wide
-    list, 7000 past it (the exact path).  The set and order must equal the oracle's either way
-    (U(0, 1) scores, the sample's tokens in [t, t + 1e-3] with t leaving ~target keys above)."""
+    list, 7000 past it (the threshold raised from the stored or published keys, the row collected
+    once more).  The set and order must equal the oracle's either way (U(0, 1) scores, the
+    sample's tokens in [t, t + 1e-3] with t leaving ~target keys above)."""
     L, B = 131072, 4
     g = torch.Generator().manual_seed(target)
     x = torch.rand(B, L, generator=g) * 0.999 + 0.001
