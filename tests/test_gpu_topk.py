@@ -109,6 +109,42 @@ def test_topk_wide_rows_sample_misses(gpu, target):
         assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"target {target} impl {name}"
 
 
+@pytest.mark.parametrize("W,target", [(65536, 4600), (65536, 9000), (131072, 7000)])
+def test_topk_second_pass_masked_blocks(gpu, W, target):
+    """The second collection pass (rows whose sampled threshold collects more keys than the
+    candidate list holds: 4096 entries up to 80K-wide scores, 5120 past it) on masked rows: 5% of
+    the tokens are masked out and hold NaN or 5.0 (above every kept score), which neither pass may
+    take.  Both list sizes, the row and split kernels, and the block-table form, whose table here
+    expands to the page table the other forms read."""
+    B = 4
+    g = torch.Generator().manual_seed(W + target)
+    x = torch.rand(B, W, generator=g) * 0.999 + 0.001
+    t = 1.0 - target / W
+    idx = torch.from_numpy((_sample_chunks(W)[:, None] + np.arange(16)[None, :]).reshape(-1))
+    for r in range(B):
+        x[r, idx] = t + torch.rand(idx.numel(), generator=g) * 1e-3
+    keep = torch.rand(B, W, generator=g) >= 0.05
+    drop = ~keep
+    x[drop] = torch.where(torch.rand(int(drop.sum()), generator=g) < 0.5, torch.tensor(float("nan")),
+                          torch.tensor(5.0))
+    w16 = torch.tensor([1 << i for i in range(16)], dtype=torch.int32)
+    bits = (keep.view(B, W // 16, 16).to(torch.int32) * w16).sum(-1, dtype=torch.int32)
+    mask = torch.where(bits > 32767, bits - 65536, bits).to(torch.int16).contiguous()
+    lengths = torch.tensor([W, W - 5, W - 4096, W - 77], dtype=torch.int32)
+    bt = torch.randperm(B * W // 64 + 5, generator=g)[:B * W // 64].view(B, W // 64).to(torch.int32)
+    tok = torch.arange(W, dtype=torch.int64)
+    pt = (bt.long()[:, tok // 64] * 64 + tok % 64).to(torch.int32)
+    ref = np.asarray(_oracle(x, mask, lengths, pt, W))
+    xg, mg, lg, pg, bg = x.to(gpu), mask.to(gpu), lengths.to(gpu), pt.to(gpu), bt.to(gpu)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=gpu)
+    for name in ("single", "s2", "s8"):
+        got = IMPLS[name](xg, mg, lg, pg, cu)
+        assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"W={W} target {target} impl {name}"
+    for splits in (1, 8):
+        got = _C.sparse_mask_topk_transform_blocks(xg, mg, lg, bg, cu, 2048, splits, None, False)
+        assert np.array_equal(np.asarray(got.cpu().numpy()), ref), f"W={W} target {target} blocks, splits {splits}"
+
+
 def test_topk_many_rows_and_empty(gpu):
     x, mask, lengths, pt = wl.topk_scores(600, 5000, "relu_sum", W=5056, ragged=True, seed=1)
     ref = np.asarray(_oracle(x, mask, lengths, pt, 5056))
