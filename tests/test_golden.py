@@ -1,0 +1,41 @@
+"""The oracle against the known-answer fixtures of tests/golden/ (written by
+tests/golden/make_golden.py from torch's fp8 / bf16 casts, exact float64 dot products and a
+brute-force top-k on the reference's key order, none of it from oracle/): the C radix top-k row
+for row, order included; the numpy top-k as a set; q quantisation, the 132-B dequant and the
+mask bit-exact; the logits to float64 rounding."""
+import os
+
+import numpy as np
+
+from oracle import indexer as O
+from oracle.topk_c import topk_radix
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    return np.load(os.path.join(GOLDEN, name))
+
+
+def test_golden_topk_oracles():
+    d = _load("topk_small.npz")
+    W = int(d["width"])
+    got = np.asarray(topk_radix(d["score"], d["mask"], d["lengths"], d["page_table"], W))
+    assert np.array_equal(got, d["expected"])
+    sets = O.topk_transform(d["score"], d["mask"], d["lengths"], d["page_table"], W)
+    assert np.array_equal(np.sort(sets, axis=1), np.sort(d["expected"], axis=1))
+
+
+def test_golden_quant_dequant_logits_oracles():
+    d = _load("indexer_small.npz")
+    q8, w_eff = O.quant_q(d["q_bf16"], d["w"])
+    assert np.array_equal(q8, d["q8"])
+    assert np.array_equal(w_eff.view(np.uint32), d["w_eff"].view(np.uint32))
+    assert np.array_equal(O.dequant_k_paged(d["kv_cache"], d["slots"]), d["dequant_bf16"])
+    logits, mag, _, mask = O.mqa_logits_decode(d["q8"], d["w_eff"], d["kv_cache"], d["context_lens"],
+                                               d["block_table"], int(d["group"]), int(d["width"]))
+    written = ~np.isnan(d["logits"])
+    assert np.array_equal(written, ~np.isnan(logits))
+    np.testing.assert_allclose(logits[written], d["logits"][written], rtol=1e-12, atol=0)
+    np.testing.assert_allclose(mag[written], d["magnitude"][written], rtol=1e-12, atol=0)
+    assert np.array_equal(mask, d["mask"])
