@@ -10,7 +10,10 @@ topk_small.npz    six rows of a 3072-wide score block (ties, exactly 2048 positi
 indexer_small.npz one decode group of two rows, 32 heads, three 64-token pages: bf16 q, head
                   weights, the 132-B paged K cache and block table; expected q8 codes, effective
                   weights, exact logits with their magnitudes, the mask words and the dequantised
-                  bf16 keys of the first row.
+                  bf16 keys of the first row; and bf16 keys written by the K-cache writer into a
+                  zeroed two-page cache (padded slots store nothing).
+mla_small.npz     24 slots of the 656-B MLA layout (512 fp8, 4 fp32 group scales, 64 bf16 rope) and
+                  the expected bf16 [n, 576] rows of a slot list (a padded slot gives zeros).
 """
 import os
 
@@ -62,7 +65,8 @@ def topk_fixture():
     x[2, rng.choice(3000, 2048, replace=False)] = np.abs(rng.standard_normal(2048)).astype(np.float32) + 0.01
     zero = np.flatnonzero(x[2, :3000] < 0)[::3]
     x[2, zero] = 0.0
-    # 3: 1000 positives, 700 masked-out tokens (counted as +0) fill the set, the rest negative
+    # 3: 1000 positives; 1400 masked-out tokens (+0 whatever their score, half of them 7.0) fill the
+    # set; the rest negative
     x[3] = -np.abs(x[3]) - 0.01
     pos = rng.choice(W, 1000, replace=False)
     x[3, pos] = np.abs(x[3, pos])
@@ -132,14 +136,53 @@ def indexer_fixture():
     prod = (fp8_values(kc).astype(np.float32) * scales.reshape(-1)[slots][:, None]).astype(np.float32)
     deq = torch.from_numpy(prod).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
 
+    # K-cache writer: per token the same quantisation, codes at page * 8448 + off * 128, the fp32
+    # scale at page * 8448 + 8192 + off * 4; slot < 0 stores nothing
+    k = (torch.randn(50, 128, generator=g) * 3).to(torch.bfloat16)
+    kslots = rng.permutation(128)[:50].astype(np.int32)
+    kslots[::9] = -1
+    kf = k.float().numpy()
+    kam = np.abs(kf).max(-1).astype(np.float32)
+    kcodes = torch.from_numpy((kf * (np.float32(448.0) / kam)[:, None]).astype(np.float32)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+    kscale = (kam / np.float32(448.0)).astype(np.float32)
+    written = np.zeros((2, 8448), dtype=np.uint8)
+    for i, sl in enumerate(kslots):
+        if sl < 0:
+            continue
+        pg, off = divmod(int(sl), 64)
+        written[pg, off * 128:(off + 1) * 128] = kcodes[i]
+        written[pg, 8192 + off * 4:8192 + off * 4 + 4] = kscale[i:i + 1].view(np.uint8)
+
     np.savez_compressed(os.path.join(HERE, "indexer_small.npz"), q_bf16=q.view(torch.int16).numpy().view(np.uint16),
                         w=w.numpy(), kv_cache=kv, block_table=bt, context_lens=lens, width=np.int32(W),
                         group=np.int32(G), q8=q8, w_eff=w_eff, logits=logits, magnitude=magnitude, mask=mask,
-                        slots=slots.astype(np.int32), dequant_bf16=deq)
+                        slots=slots.astype(np.int32), dequant_bf16=deq,
+                        k_bf16=k.view(torch.int16).numpy().view(np.uint16), k_slots=kslots, k_cache_written=written)
+
+
+def mla_fixture():
+    pool, n = 24, 40
+    g = torch.Generator().manual_seed(656)
+    cache = np.zeros((pool, 656), dtype=np.uint8)
+    cache[:, :512] = (torch.randn(pool, 512, generator=g) * 0.1).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    scales = (torch.rand(pool, 4, generator=g) * 0.02 + 1e-3).numpy().astype(np.float32)
+    cache[:, 512:528] = scales.view(np.uint8)
+    cache[:, 528:] = torch.randn(pool, 64, generator=g).to(torch.bfloat16).view(torch.uint8).numpy()
+    slots = torch.randint(0, pool, (n,), generator=g, dtype=torch.int32).numpy()
+    slots[5] = -1
+    rows = cache[np.maximum(slots, 0)]
+    vals = fp8_values(rows[:, :512]).astype(np.float32).reshape(n, 4, 128) * scales[np.maximum(slots, 0)][:, :, None]
+    nope = torch.from_numpy(vals.astype(np.float32).reshape(n, 512)).to(torch.bfloat16).view(torch.int16).numpy()
+    rope = np.ascontiguousarray(rows[:, 528:]).view(np.int16).reshape(n, 64)
+    out = np.concatenate([nope, rope], axis=1).view(np.uint16)
+    out[slots < 0] = 0
+    np.savez_compressed(os.path.join(HERE, "mla_small.npz"), cache=cache, slots=slots, expected=out)
 
 
 if __name__ == "__main__":
     topk_fixture()
     indexer_fixture()
-    for f in ("topk_small.npz", "indexer_small.npz"):
+    mla_fixture()
+    for f in ("topk_small.npz", "indexer_small.npz", "mla_small.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

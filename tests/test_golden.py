@@ -1,8 +1,8 @@
 """The oracle against the known-answer fixtures of tests/golden/ (written by
 tests/golden/make_golden.py from torch's fp8 / bf16 casts, exact float64 dot products and a
 brute-force top-k on the reference's key order, none of it from oracle/): the C radix top-k row
-for row, order included; the numpy top-k as a set; q quantisation, the 132-B dequant and the
-mask bit-exact; the logits to float64 rounding."""
+for row, order included; the numpy top-k as a set; q quantisation, the K-cache writer, both
+dequants and the mask bit-exact; the logits to float64 rounding."""
 import os
 
 import numpy as np
@@ -39,3 +39,12 @@ def test_golden_quant_dequant_logits_oracles():
     np.testing.assert_allclose(logits[written], d["logits"][written], rtol=1e-12, atol=0)
     np.testing.assert_allclose(mag[written], d["magnitude"][written], rtol=1e-12, atol=0)
     assert np.array_equal(mask, d["mask"])
+
+
+def test_golden_k_writer_and_mla_oracles():
+    d = _load("indexer_small.npz")
+    keep = d["k_slots"] >= 0
+    kf = (d["k_bf16"].astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(O.build_kv_cache(kf[keep], d["k_slots"][keep], 2), d["k_cache_written"])
+    m = _load("mla_small.npz")
+    assert np.array_equal(O.dequant_mla(m["cache"], m["slots"]), m["expected"])

@@ -1,7 +1,7 @@
 """The HIP path against the known-answer fixtures of tests/golden/ (see tests/golden/make_golden.py):
-top-k rows bit-exact, order included, on the one-CTA-per-row and split kernels; q quantisation
-and the 132-B dequant bit-exact; the mask words exact and the logits within 1e-3 of each
-token's magnitude A_t = s_t sum_h |w_h| relu(acc_h)."""
+top-k rows bit-exact, order included, on the one-CTA-per-row and split kernels; q quantisation,
+the K-cache writer and both dequants bit-exact; the mask words exact and the logits within 1e-3
+of each token's magnitude A_t = s_t sum_h |w_h| relu(acc_h)."""
 import os
 
 import numpy as np
@@ -53,3 +53,16 @@ def test_golden_quant_logits_dequant(gpu):
 
     deq = hcu_ops.dequant_k_paged(kv, torch.from_numpy(d["slots"]).to(gpu))
     assert np.array_equal(deq.view(torch.int16).cpu().numpy().view(np.uint16), d["dequant_bf16"])
+
+
+def test_golden_k_writer_and_mla(gpu):
+    d = _load("indexer_small.npz")
+    k = torch.from_numpy(d["k_bf16"].view(np.int16)).view(torch.bfloat16).to(gpu)
+    kv = torch.zeros(2, 64, 1, 132, dtype=torch.uint8, device=gpu)
+    hcu_ops.store_k_cache(k, torch.from_numpy(d["k_slots"]).to(gpu), kv)
+    assert np.array_equal(kv.view(2, -1).cpu().numpy(), d["k_cache_written"])
+    m = _load("mla_small.npz")
+    cache = torch.from_numpy(m["cache"]).view(torch.float8_e4m3fn).view(-1, 1, 656).to(gpu)
+    got = hcu_ops.dequantize_k_cache_paged(cache, torch.from_numpy(m["slots"]).to(gpu))
+    n = m["slots"].shape[0]
+    assert np.array_equal(got.view(n, 576).view(torch.int16).cpu().numpy().view(np.uint16), m["expected"])
