@@ -5,8 +5,9 @@ torch's casts (the reference generates its fp8 operands with torch's float -> fl
 hcu_ops/tests/test_mqa_hist.py:36,49), the dot products exactly in float64, and the top-k by a
 brute-force sort on the reference's key order (sparse_mask_topk.cu:4-7,40-43,199-234,301-345).
 
-topk_small.npz    six rows of a 3072-wide score block (ties, exactly 2048 positives, masked zeros
-                  filling the set, a short row, NaN / inf / -0.0) and their expected rows.
+topk_small.npz    seven rows of a 3072-wide score block (ties, exactly 2048 positives, masked zeros
+                  filling the set, a short row, NaN / inf / -0.0, a threshold at -0.0 below +0) and
+                  their expected rows.
 indexer_small.npz one decode group of two rows, 32 heads, three 64-token pages: bf16 q, head
                   weights, the 132-B paged K cache and block table; expected q8 codes, effective
                   weights, exact logits with their magnitudes, the mask words and the dequantised
@@ -53,11 +54,11 @@ def expected_row(keys, pt_row, length):
 
 
 def topk_fixture():
-    W, B = 3072, 6
+    W, B = 3072, 7
     rng = np.random.default_rng(2048)
     x = rng.standard_normal((B, W)).astype(np.float32)
     keep = np.ones((B, W), dtype=bool)
-    lengths = np.array([3072, 2500, 3000, 3072, 1500, 3072], dtype=np.int32)
+    lengths = np.array([3072, 2500, 3000, 3072, 1500, 3072, 2600], dtype=np.int32)
     # 1: heavy ties -- four values only, the threshold value held by hundreds of tokens
     x[1] = rng.choice(np.array([1.0, 0.5, 0.25, -1.0], dtype=np.float32), W, p=[0.3, 0.3, 0.3, 0.1])
     # 2: exactly 2048 positive keys, the rest +0 or negative
@@ -81,6 +82,12 @@ def topk_fixture():
     x[5, sp[16:24]] = -np.inf
     x[5, sp[24:32]] = -0.0
     x[5, sp[32:40]] = 0.0
+    # 6: 2000 positives, 30 x +0.0 and 40 x -0.0: the threshold is -0.0, just below +0
+    x[6] = -np.abs(x[6]) - 0.01
+    perm = rng.permutation(2600)
+    x[6, perm[:2000]] = np.abs(x[6, perm[:2000]])
+    x[6, perm[2000:2030]] = 0.0
+    x[6, perm[2030:2070]] = -0.0
     words = keep.reshape(B, W // 16, 16).astype(np.int64) << np.arange(16)
     mask = words.sum(-1).astype(np.uint16).view(np.int16)
     pt = (np.arange(W, dtype=np.int32)[None, :] * 3 + 5 + 100000 * np.arange(B, dtype=np.int32)[:, None])

@@ -48,3 +48,41 @@ def test_golden_k_writer_and_mla_oracles():
     assert np.array_equal(O.build_kv_cache(kf[keep], d["k_slots"][keep], 2), d["k_cache_written"])
     m = _load("mla_small.npz")
     assert np.array_equal(O.dequant_mla(m["cache"], m["slots"]), m["expected"])
+
+
+def test_golden_topk_rows_catch_plausible_mistakes():
+    """Planted mistakes in a restatement of the selection (on the CPU) each change some fixture row:
+    no +0 fast-path order, ties taken from the top token down, masked tokens keeping their score,
+    the -0.0 / +0 order swapped."""
+    d = _load("topk_small.npz")
+    x, mask, lengths, pt = d["score"], d["mask"], d["lengths"], d["page_table"]
+    bits = O.unpack_mask(mask, x.shape[1])
+
+    def rows(fast_path=True, ties_desc=False, use_mask=True, neg_zero_high=False):
+        out = []
+        for r in range(x.shape[0]):
+            L = int(lengths[r])
+            if L <= 2048:
+                out.append(np.array([pt[r, i] if i < L else -1 for i in range(2048)], dtype=np.int32))
+                continue
+            b = x[r, :L].view(np.uint32).astype(np.int64)
+            k = np.where(b & 0x80000000, (~b) & 0xFFFFFFFF, b | 0x80000000)
+            if neg_zero_high:
+                k = np.where(b == 0x80000000, 0x80000001, k)
+            if use_mask:
+                k = np.where(bits[r, :L], k, 0x80000000)
+            order = sorted(range(L), key=lambda t: (-int(k[t]), t))
+            chosen = order[:2048]
+            if fast_path and int((k > 0x80000000).sum()) == 2048:
+                sel = sorted(chosen)
+            else:
+                thr = k[order[2047]]
+                ties = [t for t in range(L) if k[t] == thr]
+                ties = sorted(ties, reverse=ties_desc)[:2048 - sum(1 for t in chosen if k[t] > thr)]
+                sel = sorted(t for t in chosen if k[t] > thr) + sorted(ties)
+            out.append(pt[r, sel].astype(np.int32))
+        return np.stack(out)
+
+    assert np.array_equal(rows(), d["expected"])  # the restatement itself agrees
+    for planted in ({"fast_path": False}, {"ties_desc": True}, {"use_mask": False}, {"neg_zero_high": True}):
+        assert not np.array_equal(rows(**planted), d["expected"]), planted
