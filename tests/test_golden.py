@@ -86,3 +86,37 @@ def test_golden_topk_rows_catch_plausible_mistakes():
     assert np.array_equal(rows(), d["expected"])  # the restatement itself agrees
     for planted in ({"fast_path": False}, {"ties_desc": True}, {"use_mask": False}, {"neg_zero_high": True}):
         assert not np.array_equal(rows(**planted), d["expected"]), planted
+
+
+def test_golden_logits_catch_plausible_mistakes():
+    """Planted mistakes in a restatement of the logits (on the CPU) each move some fixture logit
+    by more than the GPU tolerance (1e-3 of its magnitude): ReLU after the head weight, no key
+    scale, the other row's head weights, the key of the next token."""
+    from oracle.fp8 import fp8_decode
+    d = _load("indexer_small.npz")
+    q = fp8_decode(d["q8"]).astype(np.float64)
+    kv = d["kv_cache"]
+    slots = d["slots"].astype(np.int64)
+    codes = kv[slots // 64][np.arange(len(slots))[:, None], (slots % 64)[:, None] * 128 + np.arange(128)]
+    scale = np.ascontiguousarray(kv[slots // 64][np.arange(len(slots))[:, None],
+                                                  8192 + (slots % 64)[:, None] * 4 + np.arange(4)]).view(np.float32)[:, 0]
+    k = fp8_decode(codes).astype(np.float64)
+    w = d["w_eff"].astype(np.float64)
+    exact, mag = d["logits"], d["magnitude"]
+
+    def logits(relu_after_w=False, no_scale=False, swap_w=False, shift_key=False):
+        out = np.full_like(exact, np.nan)
+        kk = np.roll(k, -1, axis=0) if shift_key else k
+        for r in range(2):
+            L = int(d["context_lens"][r])
+            acc = q[r] @ kk[:L].T
+            wr = w[1 - r] if swap_w else w[r]
+            v = (np.maximum(wr[:, None] * acc, 0.0)).sum(0) if relu_after_w else wr @ np.maximum(acc, 0.0)
+            out[r, :L] = v * (1.0 if no_scale else scale[:L])
+        return out
+
+    written = ~np.isnan(exact)
+    assert (np.abs(logits()[written] - exact[written]) <= 1e-9 * mag[written] + 1e-300).all()
+    for planted in ({"relu_after_w": True}, {"no_scale": True}, {"swap_w": True}, {"shift_key": True}):
+        err = np.abs(logits(**planted)[written] - exact[written])
+        assert (err > 1e-3 * mag[written]).any(), planted
