@@ -43,6 +43,28 @@ def check_logits(got, ref, mag, dmag, what=""):
     return worst_mag, worst_rel
 
 
+def check_mask(got_mask, got_logits, ref_logits, mag, lens, what=""):
+    """The nonzero mask (mqa_hist.cu:209-218: bit = t < len && the logit's bits != 0) against the
+    kernel's own logits, exactly; and against the oracle's mask everywhere except at tokens whose
+    exact logit lies within the logits tolerance of zero (RTOL * A_t), where the fp32 epilogue
+    of cancelling heads may land on 0.0 exactly (measured once: a token at -3.7e-4 with A_t =
+    71 came out as 0.0) -- the logit there is still checked against the oracle by check_logits.
+    Returns the number of such tokens."""
+    got_mask = np.asarray(got_mask)
+    width = got_mask.shape[1] * 16
+    bits = O.unpack_mask(got_mask, width)
+    t = np.arange(width)[None, :]
+    inside = t < np.asarray(lens, dtype=np.int64)[:, None]
+    nonzero_bits = np.ascontiguousarray(np.asarray(got_logits, dtype=np.float32)[:, :width]).view(np.uint32) != 0
+    own = inside & nonzero_bits
+    assert np.array_equal(bits, own), f"{what}: mask bits differ from the kernel's own nonzero logits"
+    ref_bits = inside & ~np.isnan(ref_logits) & (np.nan_to_num(ref_logits) != 0.0)
+    differ = bits != ref_bits
+    near_zero = np.abs(np.nan_to_num(ref_logits)) <= RTOL * np.asarray(mag)
+    assert not (differ & ~near_zero).any(), f"{what}: mask differs from the oracle's at a logit away from zero"
+    return int(differ.sum())
+
+
 def sorted_rows(a):
     return np.sort(np.asarray(a), axis=1)
 
@@ -56,5 +78,5 @@ def oracle_q(case):
     return O.quant_q(q_bits(case.q), case.w.numpy())
 
 
-__all__ = ["RTOL", "CANCEL", "kv_np", "q_bits", "check_logits", "sorted_rows", "oracle_decode", "oracle_q",
+__all__ = ["RTOL", "CANCEL", "kv_np", "q_bits", "check_logits", "check_mask", "sorted_rows", "oracle_decode", "oracle_q",
            "fp8_decode"]

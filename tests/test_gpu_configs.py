@@ -27,7 +27,7 @@ import workloads as wl
 from oracle import indexer as O
 from oracle.topk_c import topk_radix
 
-from gpu_util import check_logits, kv_np, oracle_decode, oracle_q, q_bits
+from gpu_util import check_logits, check_mask, kv_np, oracle_decode, oracle_q, q_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -58,8 +58,8 @@ def test_decode_config_full_size(gpu, name):
     assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32)), "folded weights differ"
     ref, mag, dmag, ref_mask = oracle_decode(case, rq8, rw)
     got_mask = mask.cpu().numpy()
-    assert np.array_equal(got_mask, ref_mask), "nonzero mask differs from the oracle"
     got = logits.cpu().numpy()
+    check_mask(got_mask, got, ref, mag, case.context_lens.numpy(), f"{name} nonzero mask")
     worst = 0.0
     for r in range(case.rows):
         L = int(case.context_lens[r])

@@ -11,7 +11,7 @@ import workloads as wl
 from oracle import indexer as O
 from oracle.topk_c import topk_radix
 
-from gpu_util import check_logits, kv_np, oracle_decode, oracle_q
+from gpu_util import check_logits, check_mask, kv_np, oracle_decode, oracle_q
 
 pytestmark = pytest.mark.gpu
 
@@ -29,8 +29,8 @@ def _check_decode(case, lg, mask):
     q8, w = oracle_q(case)
     ref, mag, dmag, ref_mask = oracle_decode(case, q8, w)
     got_mask = mask.cpu().numpy()
-    assert np.array_equal(got_mask, ref_mask), "nonzero mask differs"
     got = lg.cpu().numpy()
+    check_mask(got_mask, got, ref, mag, case.context_lens.numpy(), "nonzero mask")
     for r in range(case.rows):
         L = int(case.context_lens[r])
         check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"row {r}")

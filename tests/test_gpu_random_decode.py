@@ -13,7 +13,7 @@ import hcu_ops
 import workloads as wl
 from oracle.topk_c import topk_radix
 
-from gpu_util import check_logits, oracle_decode, oracle_q
+from gpu_util import check_logits, check_mask, oracle_decode, oracle_q
 
 pytestmark = pytest.mark.gpu
 
@@ -51,8 +51,8 @@ def test_random_decode_step(gpu, seed):
     assert np.array_equal(q8.view(torch.uint8).cpu().numpy(), rq8), f"{what}: q8"
     ref, mag, dmag, ref_mask = oracle_decode(case, rq8, rw)
     got_mask = mask.cpu().numpy()
-    assert np.array_equal(got_mask, ref_mask), f"{what}: mask"
     got = lg.cpu().numpy()
+    check_mask(got_mask, got, ref, mag, case.context_lens.numpy(), f"{what}: mask")
     for r in range(case.rows):
         L = int(case.context_lens[r])
         check_logits(got[r, :L], ref[r, :L], mag[r, :L], dmag[r, :L], f"{what} row {r}")
