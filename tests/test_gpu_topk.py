@@ -293,3 +293,16 @@ def test_topk_short_rows_crowded_threshold_digit(gpu, W):
         assert not bad, f"W={W} impl={name}: rows (L, members, taken, keys) {bad[:4]}"
     got = np.asarray(hcu_ops.topk_transform(xg, lg, pg, cu, max_splits=1).cpu().numpy())
     assert np.array_equal(got, ref), f"W={W} dense"
+
+
+def test_topk_page_table_without_columns(gpu):
+    """A page table whose rows hold no entries (a zero-column view of a real table): every selected
+    or copied token maps to -1, on every path, without reading the table."""
+    x, mask, lengths, _ = wl.topk_scores(3, 5000, "mixed", W=5056, ragged=False, seed=77)
+    lengths = torch.tensor([5000, 100, 3000], dtype=torch.int32)
+    base = torch.arange(3 * 64, dtype=torch.int32).view(3, 64).to(gpu)
+    pt = base[:, :0]
+    cu = torch.arange(4, dtype=torch.int32, device=gpu)
+    for name, fn in IMPLS.items():
+        got = fn(x.to(gpu), mask.to(gpu), lengths.to(gpu), pt, cu).cpu().numpy()
+        assert (got == -1).all(), name
