@@ -2,8 +2,8 @@
 row counts (1-300), widths (2,000-200,000 tokens, on both sides of the 81,920-token list switch),
 the ten score distributions, masks or dense scores, ragged lengths, split counts 1-16, the
 block-table form, and rows whose sampled threshold sits low in the row (4,600-9,000 keys pass
-it, past the candidate lists: the second collection pass).  A larger run of the same generator
-(5,292 cases) matched the oracle everywhere."""
+it, past the candidate lists: the second collection pass).  Longer runs of the same generator
+(over 16,000 cases) matched the oracle everywhere."""
 import numpy as np
 import pytest
 import torch
